@@ -1,0 +1,266 @@
+#!/usr/bin/env python3
+"""MSDA forward + backward benchmark on one MI355X.
+
+One step = what one training step of a BEVFormer spatial-cross-attention
+layer asks of the operator: allocate the output, forward launch, zero-fill
+grad_value, allocate the two overwritten gradients, backward launch -- the
+timed region of the reference's benchmark (/root/reference/benchmarks/msda/benchmark_msda.py:85-119),
+through the same two C-ABI entry points the operator's autograd function uses.
+
+Workload: BASELINE config c2 (bs*cams 6, nq 10000, 8 heads x 32 channels,
+levels (116,200),(58,100),(29,50),(15,25), 8 points, float32), seeded
+synthetic inputs resident in HBM before timing.
+
+value = effective GB/s = algorithmic bytes of fwd+bwd / measured time per step
+(byte model: every tensor once at its storage width; see muspace_amd/workloads.py).
+The roofline entry prices the dominant kernel (the backward) against the
+8 TB/s HBM peak, from HIP events around each of its launches in the timed
+region. cpu_baseline times the oracle (a CPU restatement of the reference's
+PyTorch path) on a query subset of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+from muspace_amd.workloads import CONFIGS, HBM_PEAK_GBPS, algorithmic_bytes, make_inputs  # noqa: E402
+
+METRIC = "MSDA fwd+bwd µs/call + effective GB/s (% HBM peak), BEVFormer SCA shape"
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_c2_fp32.json"
+
+
+class Step:
+    """Preallocated inputs of one config and the launches of one step."""
+
+    def __init__(self, lib, cfg, value_dtype, geometry_dtype, device):
+        t = make_inputs(cfg, value_dtype=value_dtype, geometry_dtype=geometry_dtype, device=device)
+        self.lib = lib
+        self.value = t["value"]
+        self.shapes = t["spatial_shapes"]
+        self.starts = t["level_start_index"]
+        self.loc = t["sampling_locations"]
+        self.attn = t["attention_weights"]
+        self.grad = t["grad_output"]
+        self.out_shape = (cfg.batch, cfg.queries, cfg.heads * cfg.channels)
+
+    def forward(self):
+        out = torch.empty(self.out_shape, dtype=self.value.dtype, device=self.value.device)
+        self.lib.ms_deform_attn_forward(self.value, self.shapes, self.starts, self.loc,
+                                        self.attn, out, 64)
+        return out
+
+    def zero_grads(self):
+        gv = torch.zeros(self.value.shape, dtype=torch.float32, device=self.value.device)
+        gl = torch.empty(self.loc.shape, dtype=torch.float32, device=self.value.device)
+        ga = torch.empty(self.attn.shape, dtype=torch.float32, device=self.value.device)
+        return gv, gl, ga
+
+    def backward(self, grads):
+        gv, gl, ga = grads
+        self.lib.ms_deform_attn_backward(self.value, self.shapes, self.starts, self.loc,
+                                         self.attn, self.grad, gv, gl, ga, 64)
+
+    def run(self):
+        self.forward()
+        self.backward(self.zero_grads())
+
+
+def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True) -> dict:
+    """Time `steps` steps after `warmup`; HIP events around each launch."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        step.run()
+    torch.cuda.synchronize()
+    ev = {k: [] for k in ("fwd", "zero", "bwd")}
+
+    def mark():
+        e = torch.cuda.Event(enable_timing=True)
+        e.record(stream)
+        return e
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        if per_kernel:
+            a = mark()
+            step.forward()
+            b = mark()
+            grads = step.zero_grads()
+            c = mark()
+            step.backward(grads)
+            d = mark()
+            ev["fwd"].append((a, b))
+            ev["zero"].append((b, c))
+            ev["bwd"].append((c, d))
+        else:
+            step.run()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    res = {"ms_per_step": start.elapsed_time(end) / steps, "wall_ms_per_step": wall * 1e3 / steps}
+    if per_kernel:
+        for k, pairs in ev.items():
+            res[f"{k}_ms"] = sum(x.elapsed_time(y) for x, y in pairs) / len(pairs)
+    return res
+
+
+def cpu_baseline(cfg, queries: int) -> dict:
+    """The oracle (CPU restatement of the reference's PyTorch path) on a query subset."""
+    from oracle import msda_torch
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    sample = cfg.with_queries(queries)
+    t = make_inputs(sample, device="cpu")
+    value, shapes, loc, attn, grad = (t[k] for k in ("value", "spatial_shapes",
+                                                     "sampling_locations", "attention_weights",
+                                                     "grad_output"))
+    msda_torch.msda_forward_backward(value, shapes, loc, attn, grad)  # warmup
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        msda_torch.msda_forward_backward(value, shapes, loc, attn, grad)
+        times.append(time.perf_counter() - t0)
+    sec = sorted(times)[1]
+    # the query-proportional part dominates; scale the time to the full query count
+    full_sec = sec * cfg.queries / queries
+    fwd_b, bwd_b = algorithmic_bytes(cfg)
+    return {
+        "value": (fwd_b + bwd_b) / full_sec / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"oracle/msda_torch.py fwd+autograd bwd, float32, c2 with {queries} of {cfg.queries} "
+            f"queries per camera (all 6 cameras, full value): median of 3 = {sec * 1e3:.1f} ms, "
+            f"scaled x{cfg.queries / queries:g} to {full_sec * 1e3:.0f} ms per full step; "
+            f"{platform.processor() or platform.machine()}"
+        ),
+    }
+
+
+def read_traffic():
+    if TRAFFIC_FILE.is_file():
+        try:
+            return json.loads(TRAFFIC_FILE.read_text()).get("bwd_traffic_bytes")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-extra-configs", action="store_true")
+    parser.add_argument("--cpu-queries", type=int, default=500)
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the MSDA path shards over the batch (cameras) with "
+              "no exchange, so a multi-GPU figure adds nothing; run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+
+    from muspace_amd.runtime.native import load_native_module
+
+    lib = load_native_module()
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    print(f"[bench] inputs for {cfg.name}", file=sys.stderr, flush=True)
+    step = Step(lib, cfg, torch.float32, torch.float32, dev)
+    res = time_steps(step, args.steps, args.warmup)
+    fwd_b, bwd_b = algorithmic_bytes(cfg)
+    gbps = (fwd_b + bwd_b) / (res["ms_per_step"] * 1e-3) / 1e9
+    print(f"[bench] {cfg.name}: {res}", file=sys.stderr, flush=True)
+    del step
+    torch.cuda.empty_cache()
+
+    extra = {}
+    if not args.no_extra_configs:
+        for name, vdt in (("c1", torch.float32), ("c3", torch.float32), ("c4", torch.bfloat16),
+                          ("c4", torch.float16), ("bevformer-1l", torch.float32)):
+            c = CONFIGS[name]
+            print(f"[bench] extra {name} {vdt}", file=sys.stderr, flush=True)
+            s = Step(lib, c, vdt, torch.float32, dev)
+            r = time_steps(s, 50, 10)
+            f, b = algorithmic_bytes(c, vdt)
+            extra[f"{name}-{str(vdt).replace('torch.', '')}"] = {
+                "fwd_bwd_us": round(r["ms_per_step"] * 1e3, 1),
+                "fwd_us": round(r["fwd_ms"] * 1e3, 1),
+                "bwd_us": round(r["bwd_ms"] * 1e3, 1),
+                "zero_fill_us": round(r["zero_ms"] * 1e3, 1),
+                "effective_GBps": round((f + b) / (r["ms_per_step"] * 1e-3) / 1e9, 1),
+            }
+            del s
+            torch.cuda.empty_cache()
+        extra["bevformer-1l-published_ms"] = {"MTT S5000": 4.2387, "A100 (mmcv CUDA)": 4.0895}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(cfg, args.cpu_queries)
+
+    bwd_achieved = bwd_b / (res["bwd_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seed 2333; value, grad ~ N(0,1), locations ~ U(0,1), softmax weights)",
+        "config": {
+            "workload": f"{cfg.name}: BEVFormer SCA MSDA fwd+bwd, bs*cams {cfg.batch}, "
+                        f"nq {cfg.queries}, heads {cfg.heads}, head_dim {cfg.channels}, "
+                        f"levels {list(cfg.levels)}, points {cfg.points}",
+            "us_per_call": round(res["ms_per_step"] * 1e3, 1),
+            "fwd_us": round(res["fwd_ms"] * 1e3, 1),
+            "bwd_us": round(res["bwd_ms"] * 1e3, 1),
+            "zero_fill_us": round(res["zero_ms"] * 1e3, 1),
+            "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+            "algorithmic_bytes": {"fwd": fwd_b, "bwd": bwd_b},
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "msda_backward_rows<float,float,32,4>",
+            "achieved": round(bwd_achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(bwd_achieved / HBM_PEAK_GBPS, 4),
+            "traffic": read_traffic(),
+        },
+        "cpu_baseline": cpu,
+        "other_configs": extra,
+    }
+    print(json.dumps(line, ensure_ascii=False), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

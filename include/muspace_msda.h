@@ -1,0 +1,113 @@
+/*
+ * C-ABI of the MI355X (gfx950) multi-scale deformable attention library
+ * `libmuspace_msda.so`.
+ *
+ * These entry points replace the two TVM-FFI typed exports of the reference's
+ * native MSDA library:
+ *   ms_deform_attn_forward   /root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:507-560,627
+ *   ms_deform_attn_backward  /root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:561-626,628
+ * and the build smoke export
+ *   add_one                  /root/reference/csrc/ffi/muspace_ops.mu:40-55
+ * The reference's Python loader (/root/reference/mu_space/runtime/native.py:20-77)
+ * resolves those names through TVM-FFI; here they are plain C symbols resolved
+ * through ctypes (muspace_amd/runtime/native.py).
+ *
+ * Conventions (same ownership and stream rules as the reference boundary):
+ *  - Every pointer is a device pointer. The caller allocates every input and
+ *    output; the library keeps no state, allocates nothing and frees nothing.
+ *  - All tensors are dense and row-major ("contiguous"):
+ *      value               [batch, spatial_size, num_heads, channels]      value_dtype
+ *      spatial_shapes      [num_levels, 2] int64 (H, W), device-resident
+ *      level_start_index   [num_levels] int64, device-resident
+ *      sampling_locations  [batch, num_query, num_heads, num_levels, num_point, 2]  geometry_dtype
+ *                          ([..., 0] = x along W, [..., 1] = y along H, normalised to [0, 1])
+ *      attention_weights   [batch, num_query, num_heads, num_levels, num_point]     geometry_dtype
+ *      output              [batch, num_query, num_heads * channels]        value_dtype
+ *      grad_output         like output                                     value_dtype
+ *      grad_value          like value, float32, ACCUMULATED into: the caller zero-fills it
+ *      grad_sampling_locations  like sampling_locations, float32, fully OVERWRITTEN
+ *      grad_attention_weights   like attention_weights, float32, fully OVERWRITTEN
+ *  - geometry_dtype is MUSPACE_DTYPE_F32 or equal to value_dtype.
+ *  - Launches are ordered on `stream` (a hipStream_t; NULL = the null stream).
+ *    Nothing synchronises; asynchronous device faults are not reported here.
+ *  - Return 0 on success. On failure return a non-zero MUSPACE_E* code and set
+ *    a thread-local message readable through muspace_last_error(); no kernel
+ *    was launched in that case.
+ *  - `im2col_step` keeps the reference's validation: step = min(batch,
+ *    im2col_step) must be > 0 and divide batch (ms_deform_attn_musa.mu:523-524).
+ *    Batch chunking has no numeric effect, so the whole batch runs in one launch.
+ *  - Sampling follows torch.nn.functional.grid_sample(mode="bilinear",
+ *    padding_mode="zeros", align_corners=False) on grid = 2*loc - 1, which is
+ *    the reference PyTorch path (/root/reference/mu_space/ops/multi_scale_deformable_attn.py:26-58).
+ *  - Level metadata is read on the device. A level whose (start, H, W) would
+ *    address outside [0, spatial_size) is treated as empty (contributes zero)
+ *    instead of being read out of bounds.
+ */
+#ifndef MUSPACE_MSDA_H_
+#define MUSPACE_MSDA_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MUSPACE_MSDA_ABI_VERSION 1
+
+/* the library is built with -fvisibility=hidden; only these symbols export */
+#if defined(__GNUC__)
+#define MUSPACE_API __attribute__((visibility("default")))
+#else
+#define MUSPACE_API
+#endif
+
+/* dtype codes for value / output / grad_output and for the sampling geometry */
+#define MUSPACE_DTYPE_F32 0
+#define MUSPACE_DTYPE_F16 1
+#define MUSPACE_DTYPE_BF16 2
+
+/* return codes */
+#define MUSPACE_OK 0
+#define MUSPACE_EINVAL 1  /* bad argument: null pointer, negative size, dtype, im2col_step */
+#define MUSPACE_ERANGE 2  /* shape too large for the kernels' 32-bit intra-batch indexing */
+#define MUSPACE_ELAUNCH 3 /* the HIP runtime rejected a launch */
+
+/* Forward: output = MSDA(value, geometry). Replaces ms_deform_attn_forward
+ * (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:507-560). */
+MUSPACE_API int ms_deform_attn_forward(const void *value, int value_dtype, const int64_t *spatial_shapes,
+                           const int64_t *level_start_index, const void *sampling_locations,
+                           const void *attention_weights, int geometry_dtype, void *output,
+                           int64_t batch, int64_t spatial_size, int64_t num_heads,
+                           int64_t channels, int64_t num_levels, int64_t num_query,
+                           int64_t num_point, int64_t im2col_step, void *stream);
+
+/* Backward: accumulates grad_value, overwrites grad_sampling_locations and
+ * grad_attention_weights. Replaces ms_deform_attn_backward
+ * (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:561-626). */
+MUSPACE_API int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *spatial_shapes,
+                            const int64_t *level_start_index, const void *sampling_locations,
+                            const void *attention_weights, int geometry_dtype,
+                            const void *grad_output, float *grad_value,
+                            float *grad_sampling_locations, float *grad_attention_weights,
+                            int64_t batch, int64_t spatial_size, int64_t num_heads,
+                            int64_t channels, int64_t num_levels, int64_t num_query,
+                            int64_t num_point, int64_t im2col_step, void *stream);
+
+/* Build smoke: y[i] = x[i] + 1 for i < n (float32). Mirrors add_one
+ * (/root/reference/csrc/ffi/muspace_ops.mu:40-55). */
+MUSPACE_API int add_one(const float *x, float *y, int64_t n, void *stream);
+
+/* Message of the last failed call on this thread ("" if none). Replaces the
+ * TVM_FFI_ICHECK exception text of the reference boundary
+ * (/root/reference/csrc/ffi/tensor_utils.hpp:13-38). */
+MUSPACE_API const char *muspace_last_error(void);
+
+/* MUSPACE_MSDA_ABI_VERSION of the loaded library. No reference counterpart:
+ * lets the Python loader refuse a stale library. */
+MUSPACE_API int muspace_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MUSPACE_MSDA_H_ */

@@ -1,0 +1,404 @@
+// C-ABI entry points of libmuspace_msda.so (declared in include/muspace_msda.h).
+//
+// Host-side validation and kernel selection. Mirrors the checks of the
+// reference's TVM-FFI launchers ms_deform_attn_forward / ms_deform_attn_backward
+// (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:507-628):
+// dtype and pointer checks, dims, im2col_step > 0 and batch % step == 0.
+// Errors are returned as codes with a thread-local message instead of C++
+// exceptions, and the whole batch is one launch (the reference's per-chunk
+// loop has no numeric effect).
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+#include <initializer_list>
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/muspace_msda.h"
+#include "msda_kernels.hpp"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_error[0] = '\0';
+  return MUSPACE_OK;
+}
+
+int check_launch(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    return fail(MUSPACE_ELAUNCH, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
+  }
+  return ok();
+}
+
+struct Args {
+  int64_t batch, spatial, heads, channels, levels, queries, points, step;
+};
+
+const char *dtype_name(int d) {
+  switch (d) {
+    case MUSPACE_DTYPE_F32: return "float32";
+    case MUSPACE_DTYPE_F16: return "float16";
+    case MUSPACE_DTYPE_BF16: return "bfloat16";
+    default: return "unknown";
+  }
+}
+
+// Shared validation of both directions; fills `s` on success.
+int validate(const char *fn, const Args &a, int value_dtype, int geometry_dtype,
+             msda::Shape &s) {
+  if (value_dtype != MUSPACE_DTYPE_F32 && value_dtype != MUSPACE_DTYPE_F16 &&
+      value_dtype != MUSPACE_DTYPE_BF16) {
+    return fail(MUSPACE_EINVAL, "%s: value must be float32, float16 or bfloat16 (dtype code %d)",
+                fn, value_dtype);
+  }
+  if (geometry_dtype != MUSPACE_DTYPE_F32 && geometry_dtype != value_dtype) {
+    return fail(MUSPACE_EINVAL,
+                "%s: sampling_locations/attention_weights must be float32 or %s, got %s", fn,
+                dtype_name(value_dtype), dtype_name(geometry_dtype));
+  }
+  if (a.batch < 0 || a.spatial < 0 || a.heads <= 0 || a.channels <= 0 || a.levels < 0 ||
+      a.queries < 0 || a.points < 0) {
+    return fail(MUSPACE_EINVAL,
+                "%s: invalid dims batch=%lld spatial_size=%lld heads=%lld channels=%lld "
+                "levels=%lld queries=%lld points=%lld",
+                fn, (long long)a.batch, (long long)a.spatial, (long long)a.heads,
+                (long long)a.channels, (long long)a.levels, (long long)a.queries,
+                (long long)a.points);
+  }
+  const int64_t step = a.batch < a.step ? a.batch : a.step;
+  if (a.batch > 0 && step <= 0) {
+    return fail(MUSPACE_EINVAL, "%s: im2col_step must be positive, got %lld", fn,
+                (long long)a.step);
+  }
+  if (a.batch > 0 && a.batch % step != 0) {
+    return fail(MUSPACE_EINVAL, "%s: batch %lld is not divisible by im2col_step %lld", fn,
+                (long long)a.batch, (long long)step);
+  }
+  if (a.levels > msda::kMaxLevels) {
+    return fail(MUSPACE_EINVAL, "%s: at most %d levels are supported, got %lld", fn,
+                msda::kMaxLevels, (long long)a.levels);
+  }
+  const int64_t lp = a.levels * a.points;
+  const int64_t mc = a.heads * a.channels;
+  if (lp > (1 << 20) || mc > INT_MAX || a.spatial * mc > INT_MAX ||
+      a.queries * a.heads * lp * 2 > INT_MAX || a.batch * a.queries * a.heads > INT_MAX ||
+      a.queries * mc > INT_MAX) {
+    return fail(MUSPACE_ERANGE,
+                "%s: shape exceeds 32-bit per-batch indexing (spatial_size*heads*channels, "
+                "queries*heads*levels*points*2 and batch*queries*heads must each fit in int32)",
+                fn);
+  }
+  s.batch = static_cast<int>(a.batch);
+  s.spatial = static_cast<int>(a.spatial);
+  s.heads = static_cast<int>(a.heads);
+  s.channels = static_cast<int>(a.channels);
+  s.levels = static_cast<int>(a.levels);
+  s.queries = static_cast<int>(a.queries);
+  s.points = static_cast<int>(a.points);
+  s.lp = static_cast<int>(lp);
+  s.units = static_cast<int>(a.batch * a.queries * a.heads);
+  s.inv_points = a.points > 0 ? 1.0f / static_cast<float>(a.points) : 0.0f;
+  return ok();
+}
+
+int pow2_ceil(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+int log2_int(int v) {
+  int l = 0;
+  while ((1 << l) < v) ++l;
+  return l;
+}
+
+// Row-kernel launch plan: groups per unit, samples per group per pass, grid.
+struct Launch {
+  msda::RowPlan plan;
+  int ns;
+  int blocks;
+};
+
+Launch plan_rows(const msda::Shape &s, int kq) {
+  const int ng = msda::kWave / kq;
+  int gu = pow2_ceil(s.lp > 0 ? s.lp : 1);
+  if (gu > ng) gu = ng;
+  const int need = (s.lp + gu - 1) / gu;
+  Launch L;
+  L.ns = need <= 1 ? 1 : (need <= 2 ? 2 : 4);
+  L.plan.gu_log2 = log2_int(gu);
+  L.plan.iters = 2;
+  const int64_t units_per_wave_iter = ng / gu;
+  const int64_t wave_iters = (s.units + units_per_wave_iter - 1) / units_per_wave_iter;
+  const int64_t waves = (wave_iters + L.plan.iters - 1) / L.plan.iters;
+  const int64_t per_block = msda::kBlock / msda::kWave;
+  L.blocks = static_cast<int>((waves + per_block - 1) / per_block);
+  return L;
+}
+
+int generic_blocks(int64_t work) {
+  int64_t b = (work + msda::kBlock - 1) / msda::kBlock;
+  if (b > 65536) b = 65536;
+  if (b < 1) b = 1;
+  return static_cast<int>(b);
+}
+
+bool needs_data(const msda::Shape &s) { return s.units > 0; }
+
+bool aligned(const void *p, uintptr_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
+}
+
+// The row kernels move 16 bytes per lane (value, output, grad_output,
+// grad_value) and 8 bytes per location gradient; views with an odd storage
+// offset take the element-wise generic kernels instead.
+bool rows_aligned(std::initializer_list<const void *> ptrs16, const void *ptr8 = nullptr) {
+  for (const void *p : ptrs16) {
+    if (!aligned(p, 16)) return false;
+  }
+  return ptr8 == nullptr || aligned(ptr8, 8);
+}
+
+
+// ---------------------------------------------------------------- forward ---
+
+template <typename VT, typename GT, int C>
+void launch_forward_rows(const void *value, const int64_t *shapes, const int64_t *starts,
+                         const void *loc, const void *attn, void *out, const msda::Shape &s,
+                         hipStream_t st) {
+  constexpr int KQ = C / msda::RowTraits<VT>::kCpl;
+  const Launch L = plan_rows(s, KQ);
+  const VT *v = static_cast<const VT *>(value);
+  const GT *lc = static_cast<const GT *>(loc);
+  const GT *aw = static_cast<const GT *>(attn);
+  VT *o = static_cast<VT *>(out);
+  switch (L.ns) {
+    case 1:
+      msda::msda_forward_rows<VT, GT, C, 1>
+          <<<L.blocks, msda::kBlock, 0, st>>>(v, shapes, starts, lc, aw, o, s, L.plan);
+      break;
+    case 2:
+      msda::msda_forward_rows<VT, GT, C, 2>
+          <<<L.blocks, msda::kBlock, 0, st>>>(v, shapes, starts, lc, aw, o, s, L.plan);
+      break;
+    default:
+      msda::msda_forward_rows<VT, GT, C, 4>
+          <<<L.blocks, msda::kBlock, 0, st>>>(v, shapes, starts, lc, aw, o, s, L.plan);
+      break;
+  }
+}
+
+template <typename VT, typename GT>
+void launch_forward(const void *value, const int64_t *shapes, const int64_t *starts,
+                    const void *loc, const void *attn, void *out, const msda::Shape &s,
+                    hipStream_t st) {
+  const int rows = rows_aligned({value, out}) ? s.channels : 0;
+  switch (rows) {
+    case 16:
+      launch_forward_rows<VT, GT, 16>(value, shapes, starts, loc, attn, out, s, st);
+      return;
+    case 32:
+      launch_forward_rows<VT, GT, 32>(value, shapes, starts, loc, attn, out, s, st);
+      return;
+    case 64:
+      launch_forward_rows<VT, GT, 64>(value, shapes, starts, loc, attn, out, s, st);
+      return;
+    default:
+      msda::msda_forward_generic<VT, GT>
+          <<<generic_blocks(static_cast<int64_t>(s.units) * s.channels), msda::kBlock, 0, st>>>(
+              static_cast<const VT *>(value), shapes, starts, static_cast<const GT *>(loc),
+              static_cast<const GT *>(attn), static_cast<VT *>(out), s);
+      return;
+  }
+}
+
+// --------------------------------------------------------------- backward ---
+
+template <typename VT, typename GT, int C>
+void launch_backward_rows(const void *value, const int64_t *shapes, const int64_t *starts,
+                          const void *loc, const void *attn, const void *grad_out, float *gv,
+                          float *gl, float *ga, const msda::Shape &s, hipStream_t st) {
+  constexpr int KQ = C / msda::RowTraits<VT>::kCpl;
+  const Launch L = plan_rows(s, KQ);
+  const VT *v = static_cast<const VT *>(value);
+  const GT *lc = static_cast<const GT *>(loc);
+  const GT *aw = static_cast<const GT *>(attn);
+  const VT *go = static_cast<const VT *>(grad_out);
+  switch (L.ns) {
+    case 1:
+      msda::msda_backward_rows<VT, GT, C, 1><<<L.blocks, msda::kBlock, 0, st>>>(
+          v, shapes, starts, lc, aw, go, gv, gl, ga, s, L.plan);
+      break;
+    case 2:
+      msda::msda_backward_rows<VT, GT, C, 2><<<L.blocks, msda::kBlock, 0, st>>>(
+          v, shapes, starts, lc, aw, go, gv, gl, ga, s, L.plan);
+      break;
+    default:
+      msda::msda_backward_rows<VT, GT, C, 4><<<L.blocks, msda::kBlock, 0, st>>>(
+          v, shapes, starts, lc, aw, go, gv, gl, ga, s, L.plan);
+      break;
+  }
+}
+
+template <typename VT, typename GT>
+void launch_backward(const void *value, const int64_t *shapes, const int64_t *starts,
+                     const void *loc, const void *attn, const void *grad_out, float *gv,
+                     float *gl, float *ga, const msda::Shape &s, hipStream_t st) {
+  const int rows = rows_aligned({value, grad_out, gv}, gl) ? s.channels : 0;
+  switch (rows) {
+    case 16:
+      launch_backward_rows<VT, GT, 16>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga,
+                                       s, st);
+      return;
+    case 32:
+      launch_backward_rows<VT, GT, 32>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga,
+                                       s, st);
+      return;
+    case 64:
+      launch_backward_rows<VT, GT, 64>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga,
+                                       s, st);
+      return;
+    default:
+      msda::msda_backward_generic<VT, GT>
+          <<<generic_blocks(static_cast<int64_t>(s.units) * s.lp), msda::kBlock, 0, st>>>(
+              static_cast<const VT *>(value), shapes, starts, static_cast<const GT *>(loc),
+              static_cast<const GT *>(attn), static_cast<const VT *>(grad_out), gv, gl, ga, s);
+      return;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ms_deform_attn_forward(const void *value, int value_dtype, const int64_t *spatial_shapes,
+                           const int64_t *level_start_index, const void *sampling_locations,
+                           const void *attention_weights, int geometry_dtype, void *output,
+                           int64_t batch, int64_t spatial_size, int64_t num_heads,
+                           int64_t channels, int64_t num_levels, int64_t num_query,
+                           int64_t num_point, int64_t im2col_step, void *stream) {
+  static const char *fn = "ms_deform_attn_forward";
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  msda::Shape s;
+  if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
+  if (!needs_data(s)) return ok();
+  if (!output || ((!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+                   !attention_weights) &&
+                  s.lp > 0)) {
+    return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  using msda::bf16_t;
+  switch (value_dtype) {
+    case MUSPACE_DTYPE_F32:
+      launch_forward<float, float>(value, spatial_shapes, level_start_index, sampling_locations,
+                                   attention_weights, output, s, st);
+      break;
+    case MUSPACE_DTYPE_F16:
+      if (geometry_dtype == MUSPACE_DTYPE_F32) {
+        launch_forward<__half, float>(value, spatial_shapes, level_start_index,
+                                      sampling_locations, attention_weights, output, s, st);
+      } else {
+        launch_forward<__half, __half>(value, spatial_shapes, level_start_index,
+                                       sampling_locations, attention_weights, output, s, st);
+      }
+      break;
+    default:
+      if (geometry_dtype == MUSPACE_DTYPE_F32) {
+        launch_forward<bf16_t, float>(value, spatial_shapes, level_start_index,
+                                      sampling_locations, attention_weights, output, s, st);
+      } else {
+        launch_forward<bf16_t, bf16_t>(value, spatial_shapes, level_start_index,
+                                       sampling_locations, attention_weights, output, s, st);
+      }
+      break;
+  }
+  return check_launch(fn);
+}
+
+int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *spatial_shapes,
+                            const int64_t *level_start_index, const void *sampling_locations,
+                            const void *attention_weights, int geometry_dtype,
+                            const void *grad_output, float *grad_value,
+                            float *grad_sampling_locations, float *grad_attention_weights,
+                            int64_t batch, int64_t spatial_size, int64_t num_heads,
+                            int64_t channels, int64_t num_levels, int64_t num_query,
+                            int64_t num_point, int64_t im2col_step, void *stream) {
+  static const char *fn = "ms_deform_attn_backward";
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  msda::Shape s;
+  if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
+  if (!needs_data(s) || s.lp == 0) return ok();
+  if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+      !attention_weights || !grad_output || !grad_value || !grad_sampling_locations ||
+      !grad_attention_weights) {
+    return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  using msda::bf16_t;
+  switch (value_dtype) {
+    case MUSPACE_DTYPE_F32:
+      launch_backward<float, float>(value, spatial_shapes, level_start_index, sampling_locations,
+                                    attention_weights, grad_output, grad_value,
+                                    grad_sampling_locations, grad_attention_weights, s, st);
+      break;
+    case MUSPACE_DTYPE_F16:
+      if (geometry_dtype == MUSPACE_DTYPE_F32) {
+        launch_backward<__half, float>(value, spatial_shapes, level_start_index,
+                                       sampling_locations, attention_weights, grad_output,
+                                       grad_value, grad_sampling_locations,
+                                       grad_attention_weights, s, st);
+      } else {
+        launch_backward<__half, __half>(value, spatial_shapes, level_start_index,
+                                        sampling_locations, attention_weights, grad_output,
+                                        grad_value, grad_sampling_locations,
+                                        grad_attention_weights, s, st);
+      }
+      break;
+    default:
+      if (geometry_dtype == MUSPACE_DTYPE_F32) {
+        launch_backward<bf16_t, float>(value, spatial_shapes, level_start_index,
+                                       sampling_locations, attention_weights, grad_output,
+                                       grad_value, grad_sampling_locations,
+                                       grad_attention_weights, s, st);
+      } else {
+        launch_backward<bf16_t, bf16_t>(value, spatial_shapes, level_start_index,
+                                        sampling_locations, attention_weights, grad_output,
+                                        grad_value, grad_sampling_locations,
+                                        grad_attention_weights, s, st);
+      }
+      break;
+  }
+  return check_launch(fn);
+}
+
+int add_one(const float *x, float *y, int64_t n, void *stream) {
+  if (n < 0) return fail(MUSPACE_EINVAL, "add_one: negative size %lld", (long long)n);
+  if (n == 0) return ok();
+  if (!x || !y) return fail(MUSPACE_EINVAL, "add_one: null tensor pointer");
+  msda::add_one_kernel<<<generic_blocks(n), msda::kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+      x, y, n);
+  return check_launch("add_one");
+}
+
+const char *muspace_last_error(void) { return g_error; }
+
+int muspace_abi_version(void) { return MUSPACE_MSDA_ABI_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,222 @@
+// Device-side building blocks of the MI355X (gfx950) MSDA kernels.
+//
+// Sampling semantics are those of the reference PyTorch path
+// (/root/reference/mu_space/ops/multi_scale_deformable_attn.py:26-58): bilinear
+// grid_sample with zero padding and align_corners=False on grid = 2*loc - 1.
+// The pixel coordinate is evaluated with the exact operation sequence of
+// PyTorch's CPU grid_sample, ix = fma(x + 1, W/2, -0.5) with x = 2*loc - 1, so
+// that floor(ix) and therefore every corner choice agrees bit-for-bit with
+// that path; the reference's MUSA kernel uses loc*W - 0.5 instead
+// (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa_kernel.muh:286-287),
+// which differs in the last bit for about 15% of coordinates.
+//
+// Corners outside [0,W-1]x[0,H-1] read as zero (grid_sample "zeros" padding).
+// The reference kernel additionally skips a whole sample unless
+// -1 < h < H and -1 < w < W (…kernel.muh:289); that agrees with per-corner
+// padding everywhere except exactly at h == -1 or w == -1, where this code
+// follows grid_sample.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace msda {
+
+constexpr int kWave = 64;
+constexpr int kMaxLevels = 64;
+
+// Per-level metadata staged in LDS once per workgroup.
+struct Level {
+  int h, w, start;
+  float fh, fw;          // H and W as float (bounds tests, gradient scale)
+  float half_h, half_w;  // H/2 and W/2 (grid_sample's unnormalise factor)
+};
+
+struct Shape {
+  int batch, spatial, heads, channels, levels, queries, points;
+  int lp;     // levels * points
+  int units;  // batch * queries * heads
+  float inv_points;
+};
+
+// ---------------------------------------------------------------- dtypes ---
+
+struct bf16_t {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float to_float(float v) { return v; }
+__device__ __forceinline__ float to_float(__half v) { return __half2float(v); }
+__device__ __forceinline__ float to_float(bf16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_float(float v);
+template <>
+__device__ __forceinline__ float from_float<float>(float v) {
+  return v;
+}
+template <>
+__device__ __forceinline__ __half from_float<__half>(float v) {
+  return __float2half(v);  // round to nearest even
+}
+template <>
+__device__ __forceinline__ bf16_t from_float<bf16_t>(float v) {
+  // Round to nearest even; every NaN becomes the canonical quiet NaN 0x7FC0,
+  // as torch's float -> bfloat16 conversion does.
+  const uint32_t u = __float_as_uint(v);
+  bf16_t r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    r.bits = 0x7fc0;
+  } else {
+    r.bits = static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  }
+  return r;
+}
+
+// 16-byte vector access: 16 / sizeof(T) channels per lane.
+__device__ __forceinline__ void load16(const float *p, float (&o)[4]) {
+  const float4 v = *reinterpret_cast<const float4 *>(p);
+  o[0] = v.x;
+  o[1] = v.y;
+  o[2] = v.z;
+  o[3] = v.w;
+}
+__device__ __forceinline__ void load16(const bf16_t *p, float (&o)[8]) {
+  const uint4 v = *reinterpret_cast<const uint4 *>(p);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __uint_as_float(w[i] << 16);
+    o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void load16(const __half *p, float (&o)[8]) {
+  const uint4 v = *reinterpret_cast<const uint4 *>(p);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[i] & 0xffffu)));
+    o[2 * i + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[i] >> 16)));
+  }
+}
+
+__device__ __forceinline__ void store16(float *p, const float (&v)[4]) {
+  *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <typename T>
+__device__ __forceinline__ uint16_t bits16(T v);
+template <>
+__device__ __forceinline__ uint16_t bits16<bf16_t>(bf16_t v) {
+  return v.bits;
+}
+template <>
+__device__ __forceinline__ uint16_t bits16<__half>(__half v) {
+  return __half_as_ushort(v);
+}
+template <typename T>
+__device__ __forceinline__ void store16(T *p, const float (&v)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i] = static_cast<uint32_t>(bits16(from_float<T>(v[2 * i]))) |
+           (static_cast<uint32_t>(bits16(from_float<T>(v[2 * i + 1]))) << 16);
+  }
+  *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// ------------------------------------------------------- cross-lane sums ---
+
+#define MSDA_DPP(v, ctrl)                                                            \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (ctrl), 0xF, 0xF, \
+                                             false))
+
+// Sum over aligned groups of N consecutive lanes (N a power of two <= 64);
+// every lane of the group receives the total. Must be called with the whole
+// wavefront active.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (N >= 2) v += MSDA_DPP(v, 0xB1);   // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (N >= 4) v += MSDA_DPP(v, 0x4E);   // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (N >= 8) v += MSDA_DPP(v, 0x141);  // row_half_mirror: other quad of 8
+  if constexpr (N >= 16) v += MSDA_DPP(v, 0x140); // row_mirror: other half of 16
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, kWave);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+// --------------------------------------------------------------- staging ---
+
+// Copy level metadata into LDS. A level whose cells would fall outside
+// [0, spatial) is made empty so that no kernel ever reads out of bounds.
+__device__ __forceinline__ void stage_levels(Level *lv, const int64_t *shapes,
+                                             const int64_t *starts, const Shape &s) {
+  for (int l = threadIdx.x; l < s.levels; l += blockDim.x) {
+    const int64_t h = shapes[2 * l], w = shapes[2 * l + 1], st = starts[l];
+    const bool ok = h >= 0 && w >= 0 && st >= 0 && st + h * w <= s.spatial;
+    Level L;
+    L.h = ok ? static_cast<int>(h) : 0;
+    L.w = ok ? static_cast<int>(w) : 0;
+    L.start = ok ? static_cast<int>(st) : 0;
+    L.fh = static_cast<float>(L.h);
+    L.fw = static_cast<float>(L.w);
+    L.half_h = L.fh * 0.5f;
+    L.half_w = L.fw * 0.5f;
+    lv[l] = L;
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------------- geometry ---
+
+// One bilinear sample: corner offsets (in cells, relative to the level's first
+// cell) and the four bilinear weights with their validity masks.
+struct Tap {
+  int cell00;              // cell index of the top-left corner inside the level
+  float wx0, wx1, wy0, wy1;
+  bool x0ok, x1ok, y0ok, y1ok;
+};
+
+// grid_sample coordinate and corner selection for one sample. `live` false
+// makes every corner invalid.
+__device__ __forceinline__ Tap make_tap(float loc_x, float loc_y, const Level &L, bool live) {
+  // grid = 2*loc - 1 (one rounding, 2*loc is exact), then
+  // ix = fma(grid + 1, W/2, -0.5), the sequence PyTorch's CPU grid_sample uses.
+  const float gx = 2.0f * loc_x - 1.0f;
+  const float gy = 2.0f * loc_y - 1.0f;
+  const float ix = __builtin_fmaf(gx + 1.0f, L.half_w, -0.5f);
+  const float iy = __builtin_fmaf(gy + 1.0f, L.half_h, -0.5f);
+  // Samples with no in-bounds corner (and NaN) are dropped before the float ->
+  // int conversion, which keeps the integer corner coordinates small.
+  const bool in = live && ix >= -1.0f && ix < L.fw && iy >= -1.0f && iy < L.fh;
+  const float fx = floorf(ix), fy = floorf(iy);
+  const int x0 = in ? static_cast<int>(fx) : -2;
+  const int y0 = in ? static_cast<int>(fy) : -2;
+  Tap t;
+  t.wx1 = ix - fx;
+  t.wx0 = 1.0f - t.wx1;
+  t.wy1 = iy - fy;
+  t.wy0 = 1.0f - t.wy1;
+  t.x0ok = in && x0 >= 0;
+  t.x1ok = in && x0 + 1 < L.w;
+  t.y0ok = in && y0 >= 0;
+  t.y1ok = in && y0 + 1 < L.h;
+  t.cell00 = y0 * L.w + x0;
+  return t;
+}
+
+// Logical block index that gives each XCD a contiguous range of blocks.
+// Workgroups are handed to the 8 XCDs round-robin, so physical block i runs
+// on XCD i % 8; this bijection on [0, nblk) maps XCD x onto the x-th
+// contiguous slice, keeping neighbouring work (same batch and head) inside
+// one XCD's L2.
+__device__ __forceinline__ int xcd_logical_block(int bid, int nblk) {
+  constexpr int kXcd = 8;
+  const int x = bid % kXcd, j = bid / kXcd;
+  const int q = nblk / kXcd, r = nblk % kXcd;
+  return x * q + (x < r ? x : r) + j;
+}
+
+}  // namespace msda

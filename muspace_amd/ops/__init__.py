@@ -1,0 +1,17 @@
+"""Canonical operator exports (the MSDA path of /root/reference/mu_space/ops/__init__.py:24-28)."""
+
+from .multi_scale_deformable_attn import (
+    explain_dispatch,
+    level_start_index_from_shapes,
+    multi_scale_deformable_attn,
+    multi_scale_deformable_attn_pytorch,
+    multi_scale_deformable_attn_pytorch_compat,
+)
+
+__all__ = [
+    "explain_dispatch",
+    "level_start_index_from_shapes",
+    "multi_scale_deformable_attn",
+    "multi_scale_deformable_attn_pytorch",
+    "multi_scale_deformable_attn_pytorch_compat",
+]

@@ -1,0 +1,323 @@
+"""Canonical multi-scale deformable attention (MSDA) operator.
+
+Public contract of /root/reference/mu_space/ops/multi_scale_deformable_attn.py:
+  * ``multi_scale_deformable_attn(value, spatial_shapes, level_start_index,
+    sampling_locations, attention_weights, *, im2col_step=64, backend="auto")``
+    (reference :215-338), recording one dispatch report per call;
+  * ``multi_scale_deformable_attn_pytorch`` -- the grid_sample formulation used
+    by the ``reference`` backend and by CPU tensors (reference :26-58);
+  * ``multi_scale_deformable_attn_pytorch_compat`` -- the 4-argument mmcv
+    signature that derives ``level_start_index`` (reference :61-75);
+  * ``explain_dispatch`` (reference :341-348).
+
+On ROCm tensors the work runs in the hand-written gfx950 HIP kernels of
+``libmuspace_msda.so``. Autograd contract of ``_NativeMSDAFunction``
+(reference :101-190): gradients for value, sampling_locations and
+attention_weights, ``None`` for the metadata and ``im2col_step``; returned
+gradients take the dtypes of the inputs the function received.
+
+Dtype policy of the native path (differs from the reference on purpose):
+  * float16 and bfloat16 ``value`` are storage dtypes of the kernels; every
+    sampling coordinate, bilinear weight and accumulator is float32 (the
+    reference upcasts float16 to float32 in Python, :120-130);
+  * float32 ``sampling_locations`` / ``attention_weights`` stay float32 next to
+    a 16-bit ``value`` instead of being narrowed to it (:206-209): narrowing
+    the sampling geometry to 8 mantissa bits moves samples by up to W/256
+    pixels. 16-bit geometry of the value's own dtype is read as is.
+The ``reference`` backend keeps the reference's behaviour exactly (geometry
+cast to the value dtype before grid_sample).
+"""
+
+from __future__ import annotations
+
+import warnings
+
+import torch
+import torch.nn.functional as F
+
+from ..runtime.kernel_dispatch import (
+    NATIVE_BACKEND,
+    DispatchDecision,
+    DispatchReport,
+    explain_dispatch as _explain_dispatch,
+    is_rocm_tensor,
+    record_dispatch_report,
+)
+from ..runtime.native import NativeModuleUnavailable, native_error, native_module_proxy
+
+OPERATOR_NAME = "multi_scale_deformable_attn"
+_VALUE_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _native_extension():
+    try:
+        return native_module_proxy()
+    except NativeModuleUnavailable:
+        return None
+
+
+def multi_scale_deformable_attn_pytorch(
+    value: torch.Tensor,
+    value_spatial_shapes: torch.Tensor,
+    sampling_locations: torch.Tensor,
+    attention_weights: torch.Tensor,
+) -> torch.Tensor:
+    """MSDA as per-level ``F.grid_sample`` calls (bilinear, zeros, align_corners=False).
+
+    Same formulation as the reference path (ops:26-58): value is split into
+    levels in order (``level_start_index`` is implied), ``grid = 2*loc - 1``,
+    each level is sampled for all heads at once as a ``[bs*M, C, H, W]`` image,
+    and the ``L*P`` samples are weighted by ``attention_weights`` and summed.
+    """
+    bs, _, heads, channels = value.shape
+    _, queries, _, levels, points, _ = sampling_locations.shape
+    shapes = [(int(h), int(w)) for h, w in value_spatial_shapes.tolist()]
+    grids = 2 * sampling_locations - 1
+    per_level = []
+    for level, (feat, (h, w)) in enumerate(zip(value.split([h * w for h, w in shapes], 1), shapes)):
+        image = feat.flatten(2).transpose(1, 2).reshape(bs * heads, channels, h, w)
+        grid = grids[:, :, :, level].transpose(1, 2).flatten(0, 1)
+        per_level.append(
+            F.grid_sample(image, grid, mode="bilinear", padding_mode="zeros", align_corners=False)
+        )
+    weights = attention_weights.transpose(1, 2).reshape(bs * heads, 1, queries, levels * points)
+    sampled = torch.stack(per_level, dim=-2).flatten(-2)  # [bs*M, C, nq, L*P]
+    out = (sampled * weights).sum(-1).view(bs, heads * channels, queries)
+    return out.transpose(1, 2).contiguous()
+
+
+def level_start_index_from_shapes(value_spatial_shapes: torch.Tensor) -> torch.Tensor:
+    """``[0, cumsum(H*W)[:-1]]`` (reference ops:67-68, patcher runtime.py:389-395)."""
+    sizes = value_spatial_shapes[:, 0] * value_spatial_shapes[:, 1]
+    if sizes.numel() == 0:
+        return sizes.new_empty(0)
+    return torch.cat([sizes.new_zeros(1), sizes.cumsum(0)[:-1]])
+
+
+def multi_scale_deformable_attn_pytorch_compat(
+    value: torch.Tensor,
+    value_spatial_shapes: torch.Tensor,
+    sampling_locations: torch.Tensor,
+    attention_weights: torch.Tensor,
+) -> torch.Tensor:
+    """mmcv's 4-argument helper signature, routed through the canonical op."""
+    return multi_scale_deformable_attn(
+        value,
+        value_spatial_shapes,
+        level_start_index_from_shapes(value_spatial_shapes),
+        sampling_locations,
+        attention_weights,
+    )
+
+
+def _requires_native_backend(
+    value: torch.Tensor,
+    spatial_shapes: torch.Tensor,
+    level_start_index: torch.Tensor,
+    sampling_locations: torch.Tensor,
+    attention_weights: torch.Tensor,
+) -> bool:
+    return any(
+        is_rocm_tensor(t)
+        for t in (value, spatial_shapes, level_start_index, sampling_locations, attention_weights)
+    )
+
+
+def _native_geometry_dtype(value: torch.Tensor, *geometry: torch.Tensor) -> torch.dtype:
+    if value.dtype != torch.float32 and all(t.dtype == value.dtype for t in geometry):
+        return value.dtype
+    return torch.float32
+
+
+class _NativeMSDAFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(
+        ctx,
+        value: torch.Tensor,
+        spatial_shapes: torch.Tensor,
+        level_start_index: torch.Tensor,
+        sampling_locations: torch.Tensor,
+        attention_weights: torch.Tensor,
+        im2col_step: int,
+    ) -> torch.Tensor:
+        ext = _native_extension()
+        if ext is None:
+            raise RuntimeError("muSPACE HIP native library is unavailable")
+        ctx.im2col_step = im2col_step
+        ctx.value_dtype = value.dtype
+        ctx.sampling_dtype = sampling_locations.dtype
+        ctx.attention_dtype = attention_weights.dtype
+        geometry = _native_geometry_dtype(value, sampling_locations, attention_weights)
+        value_arg = value.contiguous()
+        sampling_arg = sampling_locations.to(geometry).contiguous()
+        attn_arg = attention_weights.to(geometry).contiguous()
+        spatial_arg = spatial_shapes.contiguous()
+        start_arg = level_start_index.contiguous()
+        output = value_arg.new_empty(
+            (value_arg.size(0), sampling_arg.size(1), value_arg.size(2) * value_arg.size(3))
+        )
+        ext.ms_deform_attn_forward(
+            value_arg, spatial_arg, start_arg, sampling_arg, attn_arg, output, im2col_step
+        )
+        ctx.save_for_backward(value_arg, spatial_arg, start_arg, sampling_arg, attn_arg)
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor) -> tuple[torch.Tensor | None, ...]:
+        ext = _native_extension()
+        if ext is None:
+            raise RuntimeError("muSPACE HIP native library is unavailable")
+        value, spatial_shapes, level_start_index, sampling_locations, attention_weights = (
+            ctx.saved_tensors
+        )
+        # gradients accumulate in float32 whatever the storage dtype; the
+        # kernels overwrite every element of the location/weight gradients,
+        # so only grad_value (scatter-added) needs zeroing
+        grad_value = torch.zeros(value.shape, dtype=torch.float32, device=value.device)
+        grad_sampling = torch.empty(
+            sampling_locations.shape, dtype=torch.float32, device=value.device
+        )
+        grad_attention = torch.empty(
+            attention_weights.shape, dtype=torch.float32, device=value.device
+        )
+        ext.ms_deform_attn_backward(
+            value,
+            spatial_shapes,
+            level_start_index,
+            sampling_locations,
+            attention_weights,
+            grad_output.to(value.dtype).contiguous(),
+            grad_value,
+            grad_sampling,
+            grad_attention,
+            ctx.im2col_step,
+        )
+        return (
+            grad_value.to(dtype=ctx.value_dtype),
+            None,
+            None,
+            grad_sampling.to(dtype=ctx.sampling_dtype),
+            grad_attention.to(dtype=ctx.attention_dtype),
+            None,
+        )
+
+
+def _validate_inputs(
+    value: torch.Tensor,
+    spatial_shapes: torch.Tensor,
+    level_start_index: torch.Tensor,
+) -> None:
+    # messages and exception types of the reference (ops:200-205)
+    if spatial_shapes.dtype != torch.int64:
+        raise TypeError("spatial_shapes must be int64")
+    if level_start_index.dtype != torch.int64:
+        raise TypeError("level_start_index must be int64")
+    if value.dtype not in _VALUE_DTYPES:
+        raise TypeError("value must be float16, bfloat16 or float32")
+
+
+def _reference_inputs(value, spatial_shapes, sampling_locations, attention_weights):
+    """The reference's normalisation (ops:206-212): geometry in the value dtype."""
+    return (
+        value.contiguous(),
+        spatial_shapes.contiguous(),
+        sampling_locations.to(dtype=value.dtype).contiguous(),
+        attention_weights.to(dtype=value.dtype).contiguous(),
+    )
+
+
+def _report(backend: str, selected: str, decision: DispatchDecision, native_available: bool,
+            reason: str | None = None, **extra) -> None:
+    record_dispatch_report(
+        DispatchReport(
+            operator=OPERATOR_NAME,
+            requested_backend=backend,
+            selected_backend=selected,
+            device=decision.device,
+            reason=decision.reason if reason is None else reason,
+            native_available=native_available,
+            **extra,
+        )
+    )
+
+
+def multi_scale_deformable_attn(
+    value: torch.Tensor,
+    spatial_shapes: torch.Tensor,
+    level_start_index: torch.Tensor,
+    sampling_locations: torch.Tensor,
+    attention_weights: torch.Tensor,
+    *,
+    im2col_step: int = 64,
+    backend: str = "auto",
+) -> torch.Tensor:
+    """Multi-scale deformable attention, ``[bs, nq, M*C]`` in ``value.dtype``.
+
+    ``backend``: ``"auto"`` (HIP kernels on ROCm tensors, the PyTorch path
+    elsewhere), ``"hip"`` (alias ``"musa"``: native kernels or an error) or
+    ``"reference"`` (the grid_sample path on any device).
+    """
+    _validate_inputs(value, spatial_shapes, level_start_index)
+    native_available = _native_extension() is not None
+    decision = _explain_dispatch(value, backend=backend, native_available=native_available)
+    if decision.backend == "error":
+        _report(backend, "error", decision, native_available)
+        detail = native_error() if not native_available and is_rocm_tensor(value) else None
+        raise RuntimeError(f"{decision.reason}: {detail}" if detail else decision.reason)
+    if decision.backend == "reference" or not _requires_native_backend(
+        value, spatial_shapes, level_start_index, sampling_locations, attention_weights
+    ):
+        reason = None if decision.backend == "reference" else "inputs do not require the native backend"
+        _report(backend, "reference", decision, native_available, reason)
+        return multi_scale_deformable_attn_pytorch(
+            *_reference_inputs(value, spatial_shapes, sampling_locations, attention_weights)
+        )
+    if sampling_locations.size(1) == 0:
+        # no queries: an empty output that still ties every input into the graph
+        output = value.new_zeros((value.size(0), 0, value.size(2) * value.size(3)))
+        _report(backend, NATIVE_BACKEND, decision, native_available)
+        return (
+            output
+            + value.sum() * 0
+            + sampling_locations.sum().to(value.dtype) * 0
+            + attention_weights.sum().to(value.dtype) * 0
+        )
+    try:
+        output = _NativeMSDAFunction.apply(
+            value,
+            spatial_shapes,
+            level_start_index,
+            sampling_locations,
+            attention_weights,
+            im2col_step,
+        )
+    except RuntimeError as exc:
+        if backend != "auto":
+            _report(backend, "error", decision, native_available, str(exc))
+            raise
+        # reference recovery policy (ops:311-338): auto falls back, recorded
+        _report(
+            backend,
+            "reference",
+            decision,
+            native_available,
+            "native backend failed; falling back to PyTorch reference",
+            native_fallback=True,
+            fallback_reason=str(exc),
+        )
+        warnings.warn(
+            f"muSPACE HIP MSDA failed ({exc}); falling back to the PyTorch reference",
+            RuntimeWarning,
+            stacklevel=2,
+        )
+        return multi_scale_deformable_attn_pytorch(
+            *_reference_inputs(value, spatial_shapes, sampling_locations, attention_weights)
+        )
+    _report(backend, NATIVE_BACKEND, decision, native_available)
+    return output
+
+
+def explain_dispatch(value: torch.Tensor, *, backend: str = "auto") -> DispatchDecision:
+    return _explain_dispatch(
+        value, backend=backend, native_available=_native_extension() is not None
+    )

@@ -1,0 +1,305 @@
+"""Loader for the MI355X C-ABI library ``libmuspace_msda.so``.
+
+Replaces the reference's TVM-FFI loader
+(/root/reference/mu_space/runtime/native.py:20-77). The public names are kept
+(``load_native_module``, ``native_function``, ``native_module_proxy``,
+``native_available``, ``native_error``, ``NativeModuleUnavailable``), but the
+library is a plain C-ABI shared object opened with :mod:`ctypes`, and every
+export is resolved once at load time instead of on every call.
+
+The callables returned for ``ms_deform_attn_forward`` / ``ms_deform_attn_backward``
+take torch tensors with the argument order of the reference exports
+(/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:507-628), check
+device, dtype, contiguity and shapes the way ``check_musa_contiguous``
+(/root/reference/csrc/ffi/tensor_utils.hpp:13-38) does, and launch on the
+caller's current HIP stream. A non-zero return code becomes ``RuntimeError``
+carrying the library's message.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from functools import lru_cache
+from importlib.resources import files
+from pathlib import Path
+from typing import Any, Callable
+
+LIBRARY_RELPATH = "native/libmuspace_msda.so"
+ABI_VERSION = 1
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+
+_c_int64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_ptr = ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/muspace_msda.h
+_EXPORTS: dict[str, tuple[Any, list[Any]]] = {
+    "muspace_abi_version": (_c_int, []),
+    "muspace_last_error": (ctypes.c_char_p, []),
+    "add_one": (_c_int, [_c_ptr, _c_ptr, _c_int64, _c_ptr]),
+    "ms_deform_attn_forward": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr],
+    ),
+    "ms_deform_attn_backward": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr],
+    ),
+}
+
+
+class NativeModuleUnavailable(RuntimeError):
+    """The package does not contain a usable libmuspace_msda.so."""
+
+
+def library_path() -> Path:
+    return Path(files("muspace_amd").joinpath(LIBRARY_RELPATH))
+
+
+def _dtype_code(dtype) -> int:
+    import torch
+
+    codes = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+    try:
+        return codes[dtype]
+    except KeyError:
+        raise RuntimeError(f"unsupported dtype {dtype}") from None
+
+
+def _check(tensor, name: str, dtypes) -> None:
+    if not getattr(tensor, "is_cuda", False):
+        raise RuntimeError(f"{name} must be a ROCm device tensor, got device {tensor.device}")
+    if tensor.dtype not in dtypes:
+        allowed = ", ".join(str(d).replace("torch.", "") for d in dtypes)
+        raise RuntimeError(f"{name} must be {allowed}, got {str(tensor.dtype).replace('torch.', '')}")
+    if not tensor.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _check_shape(tensor, name: str, shape: tuple[int, ...]) -> None:
+    if tuple(tensor.shape) != shape:
+        raise RuntimeError(f"{name} must have shape {list(shape)}, got {list(tensor.shape)}")
+
+
+class NativeLibrary:
+    """The loaded library with its exports bound once."""
+
+    def __init__(self, handle: ctypes.CDLL, path: Path) -> None:
+        self.path = path
+        self._raw: dict[str, Any] = {}
+        for name, (restype, argtypes) in _EXPORTS.items():
+            try:
+                fn = getattr(handle, name)
+            except AttributeError:
+                raise NativeModuleUnavailable(
+                    f"muSPACE native library {path.name} does not export {name!r}"
+                ) from None
+            fn.restype = restype
+            fn.argtypes = argtypes
+            self._raw[name] = fn
+        version = self._raw["muspace_abi_version"]()
+        if version != ABI_VERSION:
+            raise NativeModuleUnavailable(
+                f"muSPACE native library {path} has ABI version {version}, expected {ABI_VERSION}; "
+                "rebuild it with `python -m muspace_amd.build`"
+            )
+        self._bound: dict[str, Callable[..., Any]] = {
+            "ms_deform_attn_forward": self.ms_deform_attn_forward,
+            "ms_deform_attn_backward": self.ms_deform_attn_backward,
+            "add_one": self.add_one,
+        }
+
+    # ----------------------------------------------------------- helpers ---
+    def raw(self, name: str) -> Any:
+        """The bare ctypes function for ``name`` (pointer-level C-ABI)."""
+        try:
+            return self._raw[name]
+        except KeyError:
+            raise NativeModuleUnavailable(
+                f"muSPACE native library does not export {name!r}"
+            ) from None
+
+    def function(self, name: str) -> Callable[..., Any]:
+        try:
+            return self._bound[name]
+        except KeyError:
+            pass
+        return self.raw(name)
+
+    def last_error(self) -> str:
+        msg = self._raw["muspace_last_error"]()
+        return msg.decode("utf-8", "replace") if msg else ""
+
+    def _raise_on(self, rc: int, name: str) -> None:
+        if rc != 0:
+            raise RuntimeError(self.last_error() or f"{name} failed with code {rc}")
+
+    @staticmethod
+    def _stream(tensor) -> int:
+        import torch
+
+        return torch.cuda.current_stream(tensor.device).cuda_stream
+
+    # ------------------------------------------------------ tensor entry ---
+    def ms_deform_attn_forward(
+        self, value, spatial_shapes, level_start_index, sampling_locations,
+        attention_weights, output, im2col_step: int,
+    ) -> None:
+        """Tensor-level forward with the reference export's argument order."""
+        import torch
+
+        half = (torch.float32, torch.float16, torch.bfloat16)
+        _check(value, "value", half)
+        _check(spatial_shapes, "spatial_shapes", (torch.int64,))
+        _check(level_start_index, "level_start_index", (torch.int64,))
+        geom = (torch.float32,) if value.dtype == torch.float32 else (torch.float32, value.dtype)
+        _check(sampling_locations, "sampling_locations", geom)
+        _check(attention_weights, "attention_weights", (sampling_locations.dtype,))
+        _check(output, "out", (value.dtype,))
+        if value.dim() != 4 or sampling_locations.dim() != 6:
+            raise RuntimeError("value must be 4-D and sampling_locations 6-D")
+        batch, spatial, heads, channels = value.shape
+        levels = spatial_shapes.shape[0]
+        queries, points = sampling_locations.shape[1], sampling_locations.shape[4]
+        _check_shape(spatial_shapes, "spatial_shapes", (levels, 2))
+        _check_shape(level_start_index, "level_start_index", (levels,))
+        _check_shape(sampling_locations, "sampling_locations",
+                     (batch, queries, heads, levels, points, 2))
+        _check_shape(attention_weights, "attention_weights", (batch, queries, heads, levels, points))
+        _check_shape(output, "out", (batch, queries, heads * channels))
+        with torch.cuda.device(value.device):
+            rc = self._raw["ms_deform_attn_forward"](
+                value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
+                level_start_index.data_ptr(), sampling_locations.data_ptr(),
+                attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
+                output.data_ptr(), batch, spatial, heads, channels, levels, queries, points,
+                int(im2col_step), self._stream(value),
+            )
+        self._raise_on(rc, "ms_deform_attn_forward")
+
+    def ms_deform_attn_backward(
+        self, value, spatial_shapes, level_start_index, sampling_locations,
+        attention_weights, grad_output, grad_value, grad_sampling_locations,
+        grad_attention_weights, im2col_step: int,
+    ) -> None:
+        """Tensor-level backward with the reference export's argument order.
+
+        grad_value is accumulated into (zero-fill it first); the two other
+        gradient buffers are overwritten.
+        """
+        import torch
+
+        half = (torch.float32, torch.float16, torch.bfloat16)
+        _check(value, "value", half)
+        _check(spatial_shapes, "spatial_shapes", (torch.int64,))
+        _check(level_start_index, "level_start_index", (torch.int64,))
+        geom = (torch.float32,) if value.dtype == torch.float32 else (torch.float32, value.dtype)
+        _check(sampling_locations, "sampling_locations", geom)
+        _check(attention_weights, "attention_weights", (sampling_locations.dtype,))
+        _check(grad_output, "grad", (value.dtype,))
+        _check(grad_value, "grad_value", (torch.float32,))
+        _check(grad_sampling_locations, "grad_sampling_locations", (torch.float32,))
+        _check(grad_attention_weights, "grad_attention_weights", (torch.float32,))
+        if value.dim() != 4 or sampling_locations.dim() != 6:
+            raise RuntimeError("value must be 4-D and sampling_locations 6-D")
+        batch, spatial, heads, channels = value.shape
+        levels = spatial_shapes.shape[0]
+        queries, points = sampling_locations.shape[1], sampling_locations.shape[4]
+        _check_shape(spatial_shapes, "spatial_shapes", (levels, 2))
+        _check_shape(level_start_index, "level_start_index", (levels,))
+        _check_shape(sampling_locations, "sampling_locations",
+                     (batch, queries, heads, levels, points, 2))
+        _check_shape(attention_weights, "attention_weights", (batch, queries, heads, levels, points))
+        _check_shape(grad_output, "grad", (batch, queries, heads * channels))
+        _check_shape(grad_value, "grad_value", tuple(value.shape))
+        _check_shape(grad_sampling_locations, "grad_sampling_locations",
+                     tuple(sampling_locations.shape))
+        _check_shape(grad_attention_weights, "grad_attention_weights",
+                     tuple(attention_weights.shape))
+        with torch.cuda.device(value.device):
+            rc = self._raw["ms_deform_attn_backward"](
+                value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
+                level_start_index.data_ptr(), sampling_locations.data_ptr(),
+                attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
+                grad_output.data_ptr(), grad_value.data_ptr(),
+                grad_sampling_locations.data_ptr(), grad_attention_weights.data_ptr(),
+                batch, spatial, heads, channels, levels, queries, points,
+                int(im2col_step), self._stream(value),
+            )
+        self._raise_on(rc, "ms_deform_attn_backward")
+
+    def add_one(self, value, actual) -> None:
+        """Build smoke: actual = value + 1 (float32 device tensors)."""
+        import torch
+
+        _check(value, "value", (torch.float32,))
+        _check(actual, "actual", (torch.float32,))
+        if value.numel() != actual.numel():
+            raise RuntimeError("value and actual must have the same number of elements")
+        with torch.cuda.device(value.device):
+            rc = self._raw["add_one"](
+                value.data_ptr(), actual.data_ptr(), value.numel(), self._stream(value)
+            )
+        self._raise_on(rc, "add_one")
+
+
+@lru_cache(maxsize=1)
+def load_native_module() -> NativeLibrary:
+    # torch first: its bundled HIP runtime then satisfies the library's
+    # libamdhip64.so.7 dependency, so both share one runtime, device context
+    # and stream namespace.
+    import torch  # noqa: F401
+
+    library = library_path()
+    if not library.is_file():
+        raise NativeModuleUnavailable(
+            f"muSPACE native library is missing from this installation ({library}); "
+            "build it with `python -m muspace_amd.build`."
+        )
+    try:
+        handle = ctypes.CDLL(str(library))
+    except OSError as exc:
+        raise NativeModuleUnavailable(
+            f"unable to load muSPACE native library {library}: {exc}"
+        ) from exc
+    return NativeLibrary(handle, library)
+
+
+def native_function(name: str) -> Callable[..., Any]:
+    return load_native_module().function(name)
+
+
+class NativeModuleProxy:
+    """Attribute-compatible view used by the operator wrappers."""
+
+    def __getattr__(self, name: str) -> Any:
+        if name.startswith("__"):
+            raise AttributeError(name)
+        return native_function(name)
+
+
+@lru_cache(maxsize=1)
+def native_module_proxy() -> NativeModuleProxy:
+    load_native_module()
+    return NativeModuleProxy()
+
+
+def native_available() -> bool:
+    try:
+        load_native_module()
+    except NativeModuleUnavailable:
+        return False
+    return True
+
+
+def native_error() -> str | None:
+    try:
+        load_native_module()
+    except NativeModuleUnavailable as exc:
+        return str(exc)
+    return None

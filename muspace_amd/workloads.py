@@ -1,0 +1,163 @@
+"""Seeded MSDA workloads: the benchmark configurations and their byte model.
+
+Plays the role of the reference's benchmark case module
+(/root/reference/benchmarks/msda/msda_single_level_case.py:41-82) for the
+configurations this build is measured on:
+
+  c0  forward only, 4 levels (32,32),(16,16),(8,8),(4,4), bs 1, nq 1000, P 4
+  c1  Deformable-DETR encoder, 4 levels (100,167)...(13,21), bs 2, nq 22223, P 4
+  c2  BEVFormer spatial cross-attention, 4 levels (116,200)...(15,25), bs 6, nq 10000, P 8
+  c3  BEVFormer temporal self-attention, 1 level (200,200), bs 2, nq 40000, P 4
+  c4  c2's levels at bs 12, nq 15000, 16-bit value with float32 geometry
+  bevformer-1l  the reference's own published case (value scale 1.38,
+      attention weights 0.25, locations U(-0.0175, 1.0175); the reference
+      draws a separate backward set, here one set serves both directions)
+
+All have 8 heads of 32 channels. Tensors are drawn on the CPU in float32 from
+``torch.Generator("cpu").manual_seed(seed)`` in the order value, locations,
+attention logits (softmax over the L*P samples of each query and head),
+grad_output, then cast and moved.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+DEFAULT_SEED = 2333
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+
+_SCA_LEVELS = ((116, 200), (58, 100), (29, 50), (15, 25))
+
+
+@dataclass(frozen=True)
+class MSDAConfig:
+    name: str
+    batch: int
+    queries: int
+    levels: tuple[tuple[int, int], ...]
+    points: int
+    loc_low: float
+    loc_high: float
+    heads: int = 8
+    channels: int = 32
+    grid_locations: bool = False  # c3: query grid position + N(0, 0.02)
+    backward: bool = True
+    value_scale: float = 1.0
+    constant_attention: float | None = None
+    description: str = ""
+
+    @property
+    def spatial_size(self) -> int:
+        return sum(h * w for h, w in self.levels)
+
+    @property
+    def num_levels(self) -> int:
+        return len(self.levels)
+
+    def with_queries(self, queries: int) -> "MSDAConfig":
+        return MSDAConfig(**{**self.__dict__, "queries": queries})
+
+    def with_batch(self, batch: int) -> "MSDAConfig":
+        return MSDAConfig(**{**self.__dict__, "batch": batch})
+
+
+CONFIGS: dict[str, MSDAConfig] = {
+    "c0": MSDAConfig(
+        "c0", 1, 1000, ((32, 32), (16, 16), (8, 8), (4, 4)), 4, -0.05, 1.05,
+        backward=False, description="forward only, CPU-runnable",
+    ),
+    "c1": MSDAConfig(
+        "c1", 2, 22223, ((100, 167), (50, 84), (25, 42), (13, 21)), 4, -0.05, 1.05,
+        description="Deformable-DETR encoder",
+    ),
+    "c2": MSDAConfig(
+        "c2", 6, 10000, _SCA_LEVELS, 8, 0.0, 1.0,
+        description="BEVFormer spatial cross-attention",
+    ),
+    "c3": MSDAConfig(
+        "c3", 2, 40000, ((200, 200),), 4, -0.05, 1.05, grid_locations=True,
+        description="BEVFormer temporal self-attention",
+    ),
+    "c4": MSDAConfig(
+        "c4", 12, 15000, _SCA_LEVELS, 8, 0.0, 1.0,
+        description="BEVFormer spatial cross-attention, 16-bit value, fp32 geometry",
+    ),
+    "bevformer-1l": MSDAConfig(
+        "bevformer-1l", 2, 40000, ((200, 200),), 4, -0.0175, 1.0175,
+        value_scale=1.38, constant_attention=0.25,
+        description="the reference's published single-level case",
+    ),
+}
+
+
+def level_start_index(levels) -> torch.Tensor:
+    sizes = [h * w for h, w in levels]
+    starts = [0]
+    for s in sizes[:-1]:
+        starts.append(starts[-1] + s)
+    return torch.tensor(starts[: len(sizes)], dtype=torch.int64)
+
+
+def make_inputs(
+    cfg: MSDAConfig,
+    *,
+    seed: int = DEFAULT_SEED,
+    value_dtype: torch.dtype = torch.float32,
+    geometry_dtype: torch.dtype = torch.float32,
+    device: str | torch.device = "cpu",
+    with_grad_output: bool = True,
+) -> dict[str, torch.Tensor]:
+    """Seeded inputs of ``cfg`` (see module docstring for the draw order)."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    bs, nq, M, C, P, L = cfg.batch, cfg.queries, cfg.heads, cfg.channels, cfg.points, cfg.num_levels
+    value = torch.randn((bs, cfg.spatial_size, M, C), generator=gen) * cfg.value_scale
+    if cfg.grid_locations:
+        (h, w), = cfg.levels
+        idx = torch.arange(nq)
+        centre = torch.stack([(idx % w + 0.5) / w, (idx // w + 0.5) / h], dim=-1)
+        noise = torch.randn((bs, nq, M, L, P, 2), generator=gen) * 0.02
+        loc = (centre.view(1, nq, 1, 1, 1, 2) + noise).clamp_(cfg.loc_low, cfg.loc_high)
+    else:
+        loc = torch.rand((bs, nq, M, L, P, 2), generator=gen)
+        loc = loc * (cfg.loc_high - cfg.loc_low) + cfg.loc_low
+    if cfg.constant_attention is not None:
+        attn = torch.full((bs, nq, M, L, P), cfg.constant_attention)
+    else:
+        logits = torch.randn((bs, nq, M, L * P), generator=gen)
+        attn = torch.softmax(logits, dim=-1).view(bs, nq, M, L, P)
+    out = {
+        "value": value.to(value_dtype).to(device),
+        "spatial_shapes": torch.tensor(cfg.levels, dtype=torch.int64).to(device),
+        "level_start_index": level_start_index(cfg.levels).to(device),
+        "sampling_locations": loc.to(geometry_dtype).to(device),
+        "attention_weights": attn.to(geometry_dtype).to(device),
+    }
+    if with_grad_output:
+        grad = torch.randn((bs, nq, M * C), generator=gen)
+        out["grad_output"] = grad.to(value_dtype).to(device)
+    return out
+
+
+def algorithmic_bytes(
+    cfg: MSDAConfig,
+    value_dtype: torch.dtype = torch.float32,
+    geometry_dtype: torch.dtype = torch.float32,
+) -> tuple[int, int]:
+    """(forward, backward) algorithmic bytes: every tensor once at its storage width.
+
+    fwd = |value| + |loc| + |attn| + |out|
+    bwd = |value| + |loc| + |attn| + |grad_out| + |grad_value f32| + |grad_loc f32| + |grad_attn f32|
+    Zero-fills, dtype casts and repeated gathers of the same value rows are
+    not counted.
+    """
+    vb = torch.empty((), dtype=value_dtype).element_size()
+    gb = torch.empty((), dtype=geometry_dtype).element_size()
+    n_value = cfg.batch * cfg.spatial_size * cfg.heads * cfg.channels
+    n_attn = cfg.batch * cfg.queries * cfg.heads * cfg.num_levels * cfg.points
+    n_loc = 2 * n_attn
+    n_out = cfg.batch * cfg.queries * cfg.heads * cfg.channels
+    fwd = n_value * vb + n_loc * gb + n_attn * gb + n_out * vb
+    bwd = n_value * vb + n_loc * gb + n_attn * gb + n_out * vb + 4 * (n_value + n_loc + n_attn)
+    return fwd, bwd

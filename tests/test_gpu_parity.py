@@ -1,0 +1,274 @@
+"""Parity of the HIP kernels with the oracle, called through the C-ABI.
+
+Tolerances (torch.testing.assert_close semantics, |a-e| <= atol + rtol*|e|):
+  float32 forward 1e-5, float32 backward 1e-4 (atomic accumulation order is
+  nondeterministic), float16/bfloat16 value 1e-2 against the float32 oracle
+  evaluated on the same 16-bit-quantised value.
+
+Full BASELINE shapes are checked on a seeded subset of queries (every query's
+output and location/weight gradients depend only on that query, so the oracle
+on the subset is exact), grad_value with grad_output masked to that subset,
+and at full size through the adjoint identities <g, out> = <value, dvalue> =
+<attn, dattn>, which hold because MSDA is linear in value and in attention.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import gpu_available
+from msda_testlib import level_starts, max_violation
+from muspace_amd.workloads import CONFIGS, make_inputs
+from oracle import msda_torch
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not gpu_available(), reason="AMD GPU required"),
+]
+
+DEV = "cuda"
+TOL = {torch.float32: (1e-5, 1e-4), torch.float16: (1e-2, 1e-2), torch.bfloat16: (1e-2, 1e-2)}
+
+
+def _assert_close(actual, expected, tol, what):
+    actual = actual.detach().double().cpu()
+    expected = expected.detach().double().cpu()
+    viol = max_violation(actual.numpy(), expected.numpy(), tol, tol)
+    assert viol <= 0, (
+        f"{what}: max |diff| {float((actual - expected).abs().max()):.3e} exceeds tolerance {tol}"
+    )
+
+
+def run_forward(lib, t, value_dtype, geometry_dtype, im2col_step=64):
+    value = t["value"].to(value_dtype).to(DEV).contiguous()
+    loc = t["sampling_locations"].to(geometry_dtype).to(DEV).contiguous()
+    attn = t["attention_weights"].to(geometry_dtype).to(DEV).contiguous()
+    shapes, starts = t["spatial_shapes"].to(DEV), t["level_start_index"].to(DEV)
+    out = torch.empty((value.shape[0], loc.shape[1], value.shape[2] * value.shape[3]),
+                      dtype=value_dtype, device=DEV)
+    lib.ms_deform_attn_forward(value, shapes, starts, loc, attn, out, im2col_step)
+    return out
+
+
+def run_backward(lib, t, grad, value_dtype, geometry_dtype, im2col_step=64):
+    value = t["value"].to(value_dtype).to(DEV).contiguous()
+    loc = t["sampling_locations"].to(geometry_dtype).to(DEV).contiguous()
+    attn = t["attention_weights"].to(geometry_dtype).to(DEV).contiguous()
+    shapes, starts = t["spatial_shapes"].to(DEV), t["level_start_index"].to(DEV)
+    gv = torch.zeros(value.shape, dtype=torch.float32, device=DEV)
+    # poisoned: every element must be overwritten
+    gl = torch.full(loc.shape, float("nan"), dtype=torch.float32, device=DEV)
+    ga = torch.full(attn.shape, float("nan"), dtype=torch.float32, device=DEV)
+    lib.ms_deform_attn_backward(value, shapes, starts, loc, attn,
+                                grad.to(value_dtype).to(DEV).contiguous(), gv, gl, ga,
+                                im2col_step)
+    return gv, gl, ga
+
+
+def oracle_inputs(t, value_dtype, geometry_dtype):
+    """The oracle sees exactly what the kernel reads, upcast to float32."""
+    return (
+        t["value"].to(value_dtype).float().cpu(),
+        t["spatial_shapes"].cpu(),
+        t["sampling_locations"].to(geometry_dtype).float().cpu(),
+        t["attention_weights"].to(geometry_dtype).float().cpu(),
+    )
+
+
+def small_case(seed, batch, queries, heads, channels, levels, points, lo=-0.1, hi=1.1):
+    g = torch.Generator().manual_seed(seed)
+    L, nv = len(levels), sum(h * w for h, w in levels)
+    logits = torch.randn(batch, queries, heads, L * points, generator=g)
+    t = {
+        "value": torch.randn(batch, nv, heads, channels, generator=g),
+        "spatial_shapes": torch.tensor(levels, dtype=torch.int64),
+        "level_start_index": level_starts(levels),
+        "sampling_locations": torch.rand(batch, queries, heads, L, points, 2, generator=g)
+        * (hi - lo) + lo,
+        "attention_weights": torch.softmax(logits, -1).view(batch, queries, heads, L, points),
+    }
+    grad = torch.randn(batch, queries, heads * channels, generator=g)
+    return t, grad
+
+
+# (batch, queries, heads, channels, levels, points): reference test shapes
+# (odd channels, generic kernels) and row-kernel shapes covering every
+# samples-per-query layout (L*P = 1, 2, 3, 4, 5, 8, 12, 16, 32, 40, 64).
+SMALL = [
+    (1, 5, 2, 3, ((2, 2),), 4),
+    (2, 3, 4, 2, ((1, 3), (2, 1)), 2),
+    (1, 7, 1, 8, ((1, 1), (1, 2), (2, 2)), 3),
+    (1, 4, 2, 4, ((1, 2), (2, 1)), 2),
+    (2, 37, 8, 32, ((9, 13),), 1),
+    (2, 29, 8, 32, ((9, 13),), 2),
+    (1, 31, 3, 32, ((5, 4), (3, 3), (2, 2)), 1),
+    (2, 23, 8, 32, ((17, 11),), 4),
+    (1, 19, 5, 32, ((6, 7),), 5),
+    (3, 17, 8, 32, ((8, 9), (4, 5)), 4),
+    (1, 13, 8, 32, ((12, 7), (6, 4), (3, 2)), 4),
+    (2, 11, 8, 32, ((10, 12), (5, 6), (3, 3), (2, 2)), 4),
+    (2, 9, 8, 32, ((10, 12), (5, 6), (3, 3), (2, 2)), 8),
+    (1, 7, 4, 32, ((10, 12), (5, 6), (3, 3), (2, 2), (1, 1)), 8),
+    (1, 5, 2, 32, ((10, 12), (5, 6), (3, 3), (2, 2)), 16),
+    (2, 21, 8, 16, ((9, 10), (4, 5)), 4),
+    (2, 21, 4, 64, ((9, 10), (4, 5)), 4),
+    (1, 15, 8, 12, ((9, 10), (4, 5)), 4),
+]
+DTYPES = [
+    (torch.float32, torch.float32),
+    (torch.bfloat16, torch.float32),
+    (torch.bfloat16, torch.bfloat16),
+    (torch.float16, torch.float32),
+    (torch.float16, torch.float16),
+]
+
+
+def _id(case):
+    b, q, m, c, lv, p = case
+    return f"b{b}q{q}m{m}c{c}L{len(lv)}P{p}"
+
+
+@pytest.mark.parametrize("dtypes", DTYPES, ids=lambda d: f"{d[0]}-{d[1]}".replace("torch.", ""))
+@pytest.mark.parametrize("case", SMALL, ids=_id)
+def test_small_shapes_match_oracle(native_lib, case, dtypes):
+    value_dtype, geometry_dtype = dtypes
+    t, grad = small_case(sum(case[:4]), *case)
+    out = run_forward(native_lib, t, value_dtype, geometry_dtype)
+    gv, gl, ga = run_backward(native_lib, t, grad, value_dtype, geometry_dtype)
+    torch.cuda.synchronize()
+    o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
+        *oracle_inputs(t, value_dtype, geometry_dtype), grad.to(value_dtype).float()
+    )
+    ftol, btol = TOL[value_dtype]
+    _assert_close(out, o_out, ftol, "output")
+    _assert_close(gv, o_gv, btol, "grad_value")
+    _assert_close(gl, o_gl, btol, "grad_sampling_locations")
+    _assert_close(ga, o_ga, btol, "grad_attention_weights")
+
+
+def test_im2col_step_chunking_has_no_numeric_effect(native_lib):
+    t, grad = small_case(5, 4, 9, 8, 32, ((6, 7), (3, 4)), 4)
+    out_a = run_forward(native_lib, t, torch.float32, torch.float32, im2col_step=64)
+    out_b = run_forward(native_lib, t, torch.float32, torch.float32, im2col_step=2)
+    assert torch.equal(out_a, out_b)
+    with pytest.raises(RuntimeError, match="not divisible by im2col_step"):
+        run_forward(native_lib, t, torch.float32, torch.float32, im2col_step=3)
+
+
+def test_unaligned_views_take_the_generic_path(native_lib):
+    """A value view at an odd element offset is still computed correctly."""
+    t, grad = small_case(8, 1, 11, 8, 32, ((6, 7),), 4)
+    value = t["value"].to(DEV)
+    big = torch.empty(value.numel() + 1, device=DEV)
+    view = big[1:].view_as(value)
+    view.copy_(value)
+    loc = t["sampling_locations"].to(DEV)
+    attn = t["attention_weights"].to(DEV)
+    out = torch.empty((1, 11, 256), device=DEV)
+    native_lib.ms_deform_attn_forward(view, t["spatial_shapes"].to(DEV),
+                                      t["level_start_index"].to(DEV), loc, attn, out, 64)
+    expect = msda_torch.msda_forward(t["value"], t["spatial_shapes"], t["sampling_locations"],
+                                     t["attention_weights"])
+    _assert_close(out, expect, 1e-5, "output")
+
+
+def test_out_of_range_locations_give_zero(native_lib):
+    t, grad = small_case(3, 2, 6, 8, 32, ((5, 6), (2, 3)), 4)
+    t["sampling_locations"].fill_(-1.0)
+    out = run_forward(native_lib, t, torch.float32, torch.float32)
+    gv, gl, ga = run_backward(native_lib, t, grad, torch.float32, torch.float32)
+    for x in (out, gv, gl, ga):
+        assert torch.count_nonzero(x) == 0
+
+
+@pytest.mark.parametrize("value_dtype", [torch.float32, torch.bfloat16])
+def test_half_pixel_known_answer_2048(native_lib, value_dtype):
+    """Reference KAT (tests/ops/test_multi_scale_deformable_attn.py:430-468)."""
+    width = 1000
+    value = torch.zeros(1, width, 1, 32)
+    value[:, width // 2:] = 4096.0
+    t = {
+        "value": value,
+        "spatial_shapes": torch.tensor([[1, width]]),
+        "level_start_index": torch.zeros(1, dtype=torch.int64),
+        "sampling_locations": torch.full((1, 1, 1, 1, 1, 2), 0.5),
+        "attention_weights": torch.ones(1, 1, 1, 1, 1),
+    }
+    geometry = torch.float32 if value_dtype == torch.float32 else value_dtype
+    out = run_forward(native_lib, t, value_dtype, geometry)
+    assert torch.all(out.float().cpu() == 2048.0)
+
+
+def test_inconsistent_level_metadata_reads_nothing_out_of_bounds(native_lib):
+    """A level that claims more cells than value holds contributes zero."""
+    t, grad = small_case(4, 1, 8, 8, 32, ((4, 5), (2, 3)), 4, lo=0.1, hi=0.9)
+    bogus = dict(t)
+    bogus["spatial_shapes"] = torch.tensor([[4, 5], [200, 300]])
+    out = run_forward(native_lib, bogus, torch.float32, torch.float32)
+    only_first = dict(t)
+    only_first["attention_weights"] = t["attention_weights"].clone()
+    only_first["attention_weights"][:, :, :, 1] = 0
+    expect = msda_torch.msda_forward(t["value"], t["spatial_shapes"], t["sampling_locations"],
+                                     only_first["attention_weights"])
+    _assert_close(out, expect, 1e-5, "output")
+
+
+def test_add_one_smoke(native_lib):
+    """Mirrors /root/reference/tests/test_extension.py:5-16."""
+    value = torch.arange(4, dtype=torch.float32, device=DEV)
+    actual = torch.empty_like(value)
+    native_lib.add_one(value, actual)
+    torch.testing.assert_close(actual.cpu(), torch.arange(1, 5, dtype=torch.float32))
+
+
+# ------------------------------------------------------ BASELINE configs ---
+
+FULL = [
+    ("c1", torch.float32, torch.float32),
+    ("c2", torch.float32, torch.float32),
+    ("c3", torch.float32, torch.float32),
+    ("c4", torch.bfloat16, torch.float32),
+    ("c4", torch.float16, torch.float32),
+    ("bevformer-1l", torch.float32, torch.float32),
+]
+SUBSET = 48  # queries per config checked against the oracle
+
+
+@pytest.mark.parametrize("name,value_dtype,geometry_dtype", FULL,
+                         ids=[f"{n}-{str(v).replace('torch.', '')}" for n, v, _ in FULL])
+def test_full_config_parity(native_lib, name, value_dtype, geometry_dtype):
+    cfg = CONFIGS[name]
+    print(f"[parity] {name} {value_dtype} bs={cfg.batch} nq={cfg.queries}", flush=True)
+    t = make_inputs(cfg, value_dtype=torch.float32)
+    grad = t.pop("grad_output")
+    out = run_forward(native_lib, t, value_dtype, geometry_dtype)
+    gv, gl, ga = run_backward(native_lib, t, grad, value_dtype, geometry_dtype)
+    g = torch.Generator().manual_seed(7)
+    idx = torch.randperm(cfg.queries, generator=g)[:SUBSET].sort().values
+    mask = torch.zeros(cfg.queries, dtype=torch.bool)
+    mask[idx] = True
+    grad_masked = grad * mask.view(1, -1, 1)
+    gv_sub, _, _ = run_backward(native_lib, t, grad_masked, value_dtype, geometry_dtype)
+    torch.cuda.synchronize()
+
+    value, shapes, loc, attn = oracle_inputs(t, value_dtype, geometry_dtype)
+    gq = grad.to(value_dtype).float()
+    o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
+        value, shapes, loc[:, idx], attn[:, idx], gq[:, idx]
+    )
+    ftol, btol = TOL[value_dtype]
+    _assert_close(out.cpu()[:, idx], o_out, ftol, "output (query subset)")
+    _assert_close(gl.cpu()[:, idx], o_gl, btol, "grad_sampling_locations (query subset)")
+    _assert_close(ga.cpu()[:, idx], o_ga, btol, "grad_attention_weights (query subset)")
+    _assert_close(gv_sub, o_gv, btol, "grad_value (grad_output on the subset)")
+
+    # full size: every element written, and the adjoint identities
+    assert torch.isfinite(gl).all() and torch.isfinite(ga).all()
+    lhs = float((out.double() * grad.to(value_dtype).to(DEV).double()).sum())
+    rhs_v = float((t["value"].to(value_dtype).to(DEV).double() * gv.double()).sum())
+    rhs_a = float((attn.to(DEV).double() * ga.double()).sum())
+    scale = float((out.double().abs() * grad.to(DEV).double().abs()).sum())
+    rel = 1e-5 if value_dtype == torch.float32 else 3e-3
+    assert abs(lhs - rhs_v) <= rel * scale, (lhs, rhs_v, scale)
+    assert abs(lhs - rhs_a) <= rel * scale, (lhs, rhs_a, scale)
