@@ -14,7 +14,9 @@
  *
  * Conventions (same ownership and stream rules as the reference boundary):
  *  - Every pointer is a device pointer. The caller allocates every input and
- *    output; the library keeps no state, allocates nothing and frees nothing.
+ *    output; the library keeps no state. ms_deform_attn_backward takes
+ *    stream-ordered scratch (hipMallocAsync / hipFreeAsync on `stream`);
+ *    ms_deform_attn_backward_ws takes it from the caller instead.
  *  - All tensors are dense and row-major ("contiguous"):
  *      value               [batch, spatial_size, num_heads, channels]      value_dtype
  *      spatial_shapes      [num_levels, 2] int64 (H, W), device-resident
@@ -24,7 +26,8 @@
  *      attention_weights   [batch, num_query, num_heads, num_levels, num_point]     geometry_dtype
  *      output              [batch, num_query, num_heads * channels]        value_dtype
  *      grad_output         like output                                     value_dtype
- *      grad_value          like value, float32, ACCUMULATED into: the caller zero-fills it
+ *      grad_value          like value, float32, fully OVERWRITTEN (cells outside every
+ *                          level get zero)
  *      grad_sampling_locations  like sampling_locations, float32, fully OVERWRITTEN
  *      grad_attention_weights   like attention_weights, float32, fully OVERWRITTEN
  *  - geometry_dtype is MUSPACE_DTYPE_F32 or equal to value_dtype.
@@ -46,6 +49,7 @@
 #ifndef MUSPACE_MSDA_H_
 #define MUSPACE_MSDA_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -81,7 +85,7 @@ MUSPACE_API int ms_deform_attn_forward(const void *value, int value_dtype, const
                            int64_t channels, int64_t num_levels, int64_t num_query,
                            int64_t num_point, int64_t im2col_step, void *stream);
 
-/* Backward: accumulates grad_value, overwrites grad_sampling_locations and
+/* Backward: overwrites grad_value, grad_sampling_locations and
  * grad_attention_weights. Replaces ms_deform_attn_backward
  * (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:561-626). */
 MUSPACE_API int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *spatial_shapes,
@@ -92,6 +96,28 @@ MUSPACE_API int ms_deform_attn_backward(const void *value, int value_dtype, cons
                             int64_t batch, int64_t spatial_size, int64_t num_heads,
                             int64_t channels, int64_t num_levels, int64_t num_query,
                             int64_t num_point, int64_t im2col_step, void *stream);
+
+/* Scratch bytes ms_deform_attn_backward_ws needs for these dims (0: the shape
+ * takes the atomic fallback and needs none). No reference counterpart: the
+ * reference backward scatters with global atomics and needs no scratch. */
+MUSPACE_API size_t ms_deform_attn_backward_workspace_size(int value_dtype, int64_t batch,
+                                                          int64_t spatial_size, int64_t num_heads,
+                                                          int64_t channels, int64_t num_levels,
+                                                          int64_t num_query, int64_t num_point);
+
+/* ms_deform_attn_backward with caller-provided scratch (256-byte aligned, at
+ * least ms_deform_attn_backward_workspace_size bytes), so that it allocates
+ * nothing. Same results; replaces ms_deform_attn_backward
+ * (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:561-626)
+ * for callers that manage memory themselves (the Python operator does). */
+MUSPACE_API int ms_deform_attn_backward_ws(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_weights, int geometry_dtype, const void *grad_output,
+    float *grad_value, float *grad_sampling_locations, float *grad_attention_weights,
+    int64_t batch, int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream);
 
 /* Build smoke: y[i] = x[i] + 1 for i < n (float32). Mirrors add_one
  * (/root/reference/csrc/ffi/muspace_ops.mu:40-55). */

@@ -16,6 +16,7 @@
 #include <cstdio>
 
 #include "../../include/muspace_msda.h"
+#include "msda_backward_tiles.hpp"
 #include "msda_kernels.hpp"
 
 namespace {
@@ -228,6 +229,8 @@ void launch_forward(const void *value, const int64_t *shapes, const int64_t *sta
 
 // --------------------------------------------------------------- backward ---
 
+// Atomic fallback (shapes the tile path does not take): grad_value is zeroed
+// here, then accumulated with fp32 global atomics.
 template <typename VT, typename GT, int C>
 void launch_backward_rows(const void *value, const int64_t *shapes, const int64_t *starts,
                           const void *loc, const void *attn, const void *grad_out, float *gv,
@@ -255,9 +258,11 @@ void launch_backward_rows(const void *value, const int64_t *shapes, const int64_
 }
 
 template <typename VT, typename GT>
-void launch_backward(const void *value, const int64_t *shapes, const int64_t *starts,
-                     const void *loc, const void *attn, const void *grad_out, float *gv,
-                     float *gl, float *ga, const msda::Shape &s, hipStream_t st) {
+void launch_backward_atomic(const void *value, const int64_t *shapes, const int64_t *starts,
+                            const void *loc, const void *attn, const void *grad_out, float *gv,
+                            float *gl, float *ga, const msda::Shape &s, hipStream_t st) {
+  const int64_t n = static_cast<int64_t>(s.batch) * s.spatial * s.heads * s.channels;
+  if (n > 0) msda::zero_kernel<<<generic_blocks(n), msda::kBlock, 0, st>>>(gv, n);
   const int rows = rows_aligned({value, grad_out, gv}, gl) ? s.channels : 0;
   switch (rows) {
     case 16:
@@ -279,6 +284,193 @@ void launch_backward(const void *value, const int64_t *shapes, const int64_t *st
               static_cast<const GT *>(attn), static_cast<const VT *>(grad_out), gv, gl, ga, s);
       return;
   }
+}
+
+// Tile edge of the tile-owned backward per channel count (LDS budget of about
+// 72 KB fp32 per workgroup, two workgroups per CU).
+int tile_edge(int channels) { return channels == 64 ? 11 : 16; }
+
+size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+// Scratch layout of the tile-owned backward.
+struct TileWorkspace {
+  msda::BinPlan plan;
+  size_t counts, tile_start, gmax, records, bytes;
+};
+
+bool plan_tile_workspace(const msda::Shape &s, TileWorkspace &w) {
+  if (s.channels != 16 && s.channels != 32 && s.channels != 64) return false;
+  const int T = tile_edge(s.channels);
+  msda::BinPlan &p = w.plan;
+  p.chunk_q = msda::kBinBlock;
+  p.chunks = (s.queries + p.chunk_q - 1) / p.chunk_q;
+  // tiles of one level < 3*H*W/T + 1, so 3*spatial/T + levels + 1 bounds a slab
+  const int64_t bound = 3 * static_cast<int64_t>(s.spatial) / T + s.levels + 1;
+  if (bound > msda::kMaxTilesPerSlab) return false;
+  p.tile_bound = static_cast<int>(bound);
+  p.lp_log2 = log2_int(s.lp > 0 ? s.lp : 1);
+  if ((static_cast<int64_t>(s.queries) << p.lp_log2) > (int64_t{1} << 32)) return false;
+  p.rec_cap = 4 * static_cast<int64_t>(s.queries) * s.lp;
+  const int64_t bm = static_cast<int64_t>(s.batch) * s.heads;
+  size_t off = 0;
+  w.counts = off;
+  off = align256(off + static_cast<size_t>(bm) * p.chunks * p.tile_bound * 4);
+  w.tile_start = off;
+  off = align256(off + static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
+  w.gmax = off;
+  off = align256(off + static_cast<size_t>(s.units) * 4);
+  w.records = off;
+  off = align256(off + static_cast<size_t>(bm) * p.rec_cap * 4);
+  w.bytes = off;
+  return true;
+}
+
+// Persistent grid of the tile kernel: two workgroups per CU, a multiple of 8
+// (the XCD count) so that every XCD gets the same number of workgroups.
+int tile_grid() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0) {
+      cus = 256;
+    }
+    cached[dev] = ((2 * cus + 7) / 8) * 8;
+  }
+  return cached[dev];
+}
+
+template <typename VT, typename GT, int C>
+void launch_backward_tiles(const void *value, const int64_t *shapes, const int64_t *starts,
+                           const void *loc, const void *attn, const void *grad_out, float *gv,
+                           float *gl, float *ga, const msda::Shape &s, const TileWorkspace &w,
+                           void *workspace, hipStream_t st) {
+  constexpr int T = C == 64 ? 11 : 16;
+  unsigned char *ws = static_cast<unsigned char *>(workspace);
+  uint32_t *counts = reinterpret_cast<uint32_t *>(ws + w.counts);
+  uint32_t *tile_start = reinterpret_cast<uint32_t *>(ws + w.tile_start);
+  float *gmax = reinterpret_cast<float *>(ws + w.gmax);
+  uint32_t *records = reinterpret_cast<uint32_t *>(ws + w.records);
+  const msda::BinPlan &p = w.plan;
+  const int bm = s.batch * s.heads;
+  const VT *v = static_cast<const VT *>(value);
+  const GT *lc = static_cast<const GT *>(loc);
+  const GT *aw = static_cast<const GT *>(attn);
+  const VT *go = static_cast<const VT *>(grad_out);
+  const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4;
+
+  auto count = msda::msda_bin_count<VT, GT, C, T>;
+  auto scatter = msda::msda_bin_scatter<GT, T>;
+  auto tile = msda::msda_tile_backward<VT, GT, C, T>;
+  const size_t tile_bytes = msda::tile_lds_bytes<T>(C, sizeof(VT));
+  (void)hipFuncSetAttribute(reinterpret_cast<const void *>(count),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, hist_bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void *>(scatter),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, hist_bytes);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void *>(tile),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, tile_bytes);
+
+  count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, go, s, p, counts,
+                                                             gmax, gl, ga);
+  msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(shapes, starts, s, p, counts,
+                                                             tile_start, gv);
+  scatter<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts,
+                                                               records);
+  tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, shapes, starts, lc, aw, go, gmax,
+                                                          records, tile_start, s, p, gv, gl, ga);
+}
+
+template <typename VT, typename GT>
+void launch_backward(const void *value, const int64_t *shapes, const int64_t *starts,
+                     const void *loc, const void *attn, const void *grad_out, float *gv,
+                     float *gl, float *ga, const msda::Shape &s, void *workspace,
+                     size_t workspace_bytes, hipStream_t st) {
+  TileWorkspace w;
+  const bool tiles = plan_tile_workspace(s, w) && workspace != nullptr &&
+                     workspace_bytes >= w.bytes && rows_aligned({value, grad_out, gv}, gl) &&
+                     aligned(workspace, 256);
+  if (!tiles) {
+    launch_backward_atomic<VT, GT>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga, s, st);
+    return;
+  }
+  switch (s.channels) {
+    case 16:
+      launch_backward_tiles<VT, GT, 16>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga,
+                                        s, w, workspace, st);
+      return;
+    case 32:
+      launch_backward_tiles<VT, GT, 32>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga,
+                                        s, w, workspace, st);
+      return;
+    default:
+      launch_backward_tiles<VT, GT, 64>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga,
+                                        s, w, workspace, st);
+      return;
+  }
+}
+
+int backward_impl(const char *fn, const void *value, int value_dtype,
+                  const int64_t *spatial_shapes, const int64_t *level_start_index,
+                  const void *sampling_locations, const void *attention_weights,
+                  int geometry_dtype, const void *grad_output, float *grad_value,
+                  float *grad_sampling_locations, float *grad_attention_weights, const Args &a,
+                  void *workspace, size_t workspace_bytes, hipStream_t st) {
+  msda::Shape s;
+  if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
+  const int64_t nvalue = a.batch * a.spatial * a.heads * a.channels;
+  if (nvalue > 0 && !grad_value) return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+  if (!needs_data(s) || s.lp == 0) {
+    // nothing samples the value: its gradient is zero
+    if (nvalue > 0) {
+      msda::zero_kernel<<<generic_blocks(nvalue), msda::kBlock, 0, st>>>(grad_value, nvalue);
+      return check_launch(fn);
+    }
+    return ok();
+  }
+  if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+      !attention_weights || !grad_output || !grad_sampling_locations || !grad_attention_weights) {
+    return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+  }
+  using msda::bf16_t;
+  switch (value_dtype) {
+    case MUSPACE_DTYPE_F32:
+      launch_backward<float, float>(value, spatial_shapes, level_start_index, sampling_locations,
+                                    attention_weights, grad_output, grad_value,
+                                    grad_sampling_locations, grad_attention_weights, s,
+                                    workspace, workspace_bytes, st);
+      break;
+    case MUSPACE_DTYPE_F16:
+      if (geometry_dtype == MUSPACE_DTYPE_F32) {
+        launch_backward<__half, float>(value, spatial_shapes, level_start_index,
+                                       sampling_locations, attention_weights, grad_output,
+                                       grad_value, grad_sampling_locations,
+                                       grad_attention_weights, s, workspace, workspace_bytes, st);
+      } else {
+        launch_backward<__half, __half>(value, spatial_shapes, level_start_index,
+                                        sampling_locations, attention_weights, grad_output,
+                                        grad_value, grad_sampling_locations,
+                                        grad_attention_weights, s, workspace, workspace_bytes,
+                                        st);
+      }
+      break;
+    default:
+      if (geometry_dtype == MUSPACE_DTYPE_F32) {
+        launch_backward<bf16_t, float>(value, spatial_shapes, level_start_index,
+                                       sampling_locations, attention_weights, grad_output,
+                                       grad_value, grad_sampling_locations,
+                                       grad_attention_weights, s, workspace, workspace_bytes, st);
+      } else {
+        launch_backward<bf16_t, bf16_t>(value, spatial_shapes, level_start_index,
+                                        sampling_locations, attention_weights, grad_output,
+                                        grad_value, grad_sampling_locations,
+                                        grad_attention_weights, s, workspace, workspace_bytes,
+                                        st);
+      }
+      break;
+  }
+  return check_launch(fn);
 }
 
 }  // namespace
@@ -331,6 +523,39 @@ int ms_deform_attn_forward(const void *value, int value_dtype, const int64_t *sp
   return check_launch(fn);
 }
 
+size_t ms_deform_attn_backward_workspace_size(int value_dtype, int64_t batch,
+                                              int64_t spatial_size, int64_t num_heads,
+                                              int64_t channels, int64_t num_levels,
+                                              int64_t num_query, int64_t num_point) {
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               batch > 0 ? batch : 1};
+  msda::Shape s;
+  if (validate("ms_deform_attn_backward_workspace_size", a, value_dtype, value_dtype, s)) {
+    return 0;
+  }
+  ok();
+  TileWorkspace w;
+  if (!needs_data(s) || s.lp == 0 || !plan_tile_workspace(s, w)) return 0;
+  return w.bytes;
+}
+
+int ms_deform_attn_backward_ws(const void *value, int value_dtype, const int64_t *spatial_shapes,
+                               const int64_t *level_start_index, const void *sampling_locations,
+                               const void *attention_weights, int geometry_dtype,
+                               const void *grad_output, float *grad_value,
+                               float *grad_sampling_locations, float *grad_attention_weights,
+                               int64_t batch, int64_t spatial_size, int64_t num_heads,
+                               int64_t channels, int64_t num_levels, int64_t num_query,
+                               int64_t num_point, int64_t im2col_step, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  return backward_impl("ms_deform_attn_backward_ws", value, value_dtype, spatial_shapes,
+                       level_start_index, sampling_locations, attention_weights, geometry_dtype,
+                       grad_output, grad_value, grad_sampling_locations, grad_attention_weights,
+                       a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
 int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *spatial_shapes,
                             const int64_t *level_start_index, const void *sampling_locations,
                             const void *attention_weights, int geometry_dtype,
@@ -342,50 +567,31 @@ int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *s
   static const char *fn = "ms_deform_attn_backward";
   const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
                im2col_step};
+  hipStream_t st = static_cast<hipStream_t>(stream);
   msda::Shape s;
   if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
-  if (!needs_data(s) || s.lp == 0) return ok();
-  if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
-      !attention_weights || !grad_output || !grad_value || !grad_sampling_locations ||
-      !grad_attention_weights) {
+  if (needs_data(s) && s.lp > 0 &&
+      (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+       !attention_weights || !grad_output || !grad_value || !grad_sampling_locations ||
+       !grad_attention_weights)) {
     return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
   }
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  using msda::bf16_t;
-  switch (value_dtype) {
-    case MUSPACE_DTYPE_F32:
-      launch_backward<float, float>(value, spatial_shapes, level_start_index, sampling_locations,
-                                    attention_weights, grad_output, grad_value,
-                                    grad_sampling_locations, grad_attention_weights, s, st);
-      break;
-    case MUSPACE_DTYPE_F16:
-      if (geometry_dtype == MUSPACE_DTYPE_F32) {
-        launch_backward<__half, float>(value, spatial_shapes, level_start_index,
-                                       sampling_locations, attention_weights, grad_output,
-                                       grad_value, grad_sampling_locations,
-                                       grad_attention_weights, s, st);
-      } else {
-        launch_backward<__half, __half>(value, spatial_shapes, level_start_index,
-                                        sampling_locations, attention_weights, grad_output,
-                                        grad_value, grad_sampling_locations,
-                                        grad_attention_weights, s, st);
-      }
-      break;
-    default:
-      if (geometry_dtype == MUSPACE_DTYPE_F32) {
-        launch_backward<bf16_t, float>(value, spatial_shapes, level_start_index,
-                                       sampling_locations, attention_weights, grad_output,
-                                       grad_value, grad_sampling_locations,
-                                       grad_attention_weights, s, st);
-      } else {
-        launch_backward<bf16_t, bf16_t>(value, spatial_shapes, level_start_index,
-                                        sampling_locations, attention_weights, grad_output,
-                                        grad_value, grad_sampling_locations,
-                                        grad_attention_weights, s, st);
-      }
-      break;
+  // stream-ordered scratch of the tile-owned path; freed in stream order
+  size_t bytes = 0;
+  TileWorkspace w;
+  if (needs_data(s) && s.lp > 0 && plan_tile_workspace(s, w)) bytes = w.bytes;
+  void *workspace = nullptr;
+  if (bytes > 0 && hipMallocAsync(&workspace, bytes, st) != hipSuccess) {
+    (void)hipGetLastError();
+    workspace = nullptr;  // the atomic fallback needs no scratch
+    bytes = 0;
   }
-  return check_launch(fn);
+  const int rc = backward_impl(fn, value, value_dtype, spatial_shapes, level_start_index,
+                               sampling_locations, attention_weights, geometry_dtype, grad_output,
+                               grad_value, grad_sampling_locations, grad_attention_weights, a,
+                               workspace, bytes, st);
+  if (workspace) (void)hipFreeAsync(workspace, st);
+  return rc;
 }
 
 int add_one(const float *x, float *y, int64_t n, void *stream) {

@@ -21,6 +21,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <climits>
+
 namespace msda {
 
 constexpr int kWave = 64;
@@ -150,16 +152,32 @@ __device__ __forceinline__ float group_sum(float v) {
 // --------------------------------------------------------------- staging ---
 
 // Copy level metadata into LDS. A level whose cells would fall outside
-// [0, spatial) is made empty so that no kernel ever reads out of bounds.
+// [0, spatial), or overlap the cells of an earlier in-range level, is made
+// empty (contributes nothing): no kernel reads out of bounds, and every value
+// cell belongs to at most one level, which the tile-owned backward relies on.
 __device__ __forceinline__ void stage_levels(Level *lv, const int64_t *shapes,
                                              const int64_t *starts, const Shape &s) {
+  // [start, end) of each in-range level; end = -1 marks an out-of-range level
+  __shared__ int64_t range[kMaxLevels][2];
   for (int l = threadIdx.x; l < s.levels; l += blockDim.x) {
     const int64_t h = shapes[2 * l], w = shapes[2 * l + 1], st = starts[l];
-    const bool ok = h >= 0 && w >= 0 && st >= 0 && st + h * w <= s.spatial;
+    const bool ok = h >= 0 && w >= 0 && h <= s.spatial && w <= s.spatial && st >= 0 &&
+                    st + h * w <= s.spatial;
+    range[l][0] = st;
+    range[l][1] = ok ? st + h * w : -1;
+  }
+  __syncthreads();
+  for (int l = threadIdx.x; l < s.levels; l += blockDim.x) {
+    const int64_t a0 = range[l][0], a1 = range[l][1];
+    bool ok = a1 >= 0;
+    for (int j = 0; j < l && ok; ++j) {
+      const int64_t b0 = range[j][0], b1 = range[j][1];
+      ok = !(b1 > b0 && a1 > a0 && a0 < b1 && b0 < a1);  // no cell shared with an earlier level
+    }
     Level L;
-    L.h = ok ? static_cast<int>(h) : 0;
-    L.w = ok ? static_cast<int>(w) : 0;
-    L.start = ok ? static_cast<int>(st) : 0;
+    L.h = ok ? static_cast<int>(shapes[2 * l]) : 0;
+    L.w = ok ? static_cast<int>(shapes[2 * l + 1]) : 0;
+    L.start = ok ? static_cast<int>(a0) : 0;
     L.fh = static_cast<float>(L.h);
     L.fw = static_cast<float>(L.w);
     L.half_h = L.fh * 0.5f;
@@ -174,8 +192,10 @@ __device__ __forceinline__ void stage_levels(Level *lv, const int64_t *shapes,
 // One bilinear sample: corner offsets (in cells, relative to the level's first
 // cell) and the four bilinear weights with their validity masks.
 struct Tap {
+  int x0, y0;              // top-left corner (may be -1); meaningless unless `in`
   int cell00;              // cell index of the top-left corner inside the level
   float wx0, wx1, wy0, wy1;
+  bool in;                 // at least one corner inside the level
   bool x0ok, x1ok, y0ok, y1ok;
 };
 
@@ -195,6 +215,9 @@ __device__ __forceinline__ Tap make_tap(float loc_x, float loc_y, const Level &L
   const int x0 = in ? static_cast<int>(fx) : -2;
   const int y0 = in ? static_cast<int>(fy) : -2;
   Tap t;
+  t.x0 = x0;
+  t.y0 = y0;
+  t.in = in;
   t.wx1 = ix - fx;
   t.wx0 = 1.0f - t.wx1;
   t.wy1 = iy - fy;
@@ -205,6 +228,12 @@ __device__ __forceinline__ Tap make_tap(float loc_x, float loc_y, const Level &L
   t.y1ok = in && y0 + 1 < L.h;
   t.cell00 = y0 * L.w + x0;
   return t;
+}
+
+// Level of flat sample index smp = l * P + p. Exact for smp < 2^20: (smp + 0.5)/P
+// is at least 0.5/P away from an integer.
+__device__ __forceinline__ int level_of_sample(int smp, const Shape &s) {
+  return static_cast<int>((static_cast<float>(smp) + 0.5f) * s.inv_points);
 }
 
 // Logical block index that gives each XCD a contiguous range of blocks.

@@ -54,11 +54,6 @@ __device__ __forceinline__ Unit decode_unit(int u, const Shape &s) {
   return r;
 }
 
-__device__ __forceinline__ int level_of(int smp, const Shape &s) {
-  // exact for smp < 2^20: (smp + 0.5)/P is at least 0.5/P away from an integer
-  return static_cast<int>((static_cast<float>(smp) + 0.5f) * s.inv_points);
-}
-
 // ------------------------------------------------------------- forward ---
 
 template <typename VT, typename GT, int C, int NS>
@@ -106,7 +101,7 @@ __global__ void __launch_bounds__(kBlock)
         const int smp = s0 + gi + GU * i;
         const bool ok = live && smp < s.lp;
         const int sm = ok ? smp : 0;
-        const Level L = lv[level_of(sm, s)];
+        const Level L = lv[level_of_sample(sm, s)];
         const float a = ok ? to_float(abase[sm]) : 0.0f;
         const Tap t = make_tap(to_float(lbase[2 * sm]), to_float(lbase[2 * sm + 1]), L, ok);
         w[i][0] = a * (t.wy0 * t.wx0);
@@ -206,7 +201,7 @@ __global__ void __launch_bounds__(kBlock)
         const int smp = s0 + gi + GU * i;
         const bool ok = live && smp < s.lp;
         const int sm = ok ? smp : 0;
-        const Level L = lv[level_of(sm, s)];
+        const Level L = lv[level_of_sample(sm, s)];
         a[i] = ok ? to_float(abase[sm]) : 0.0f;
         fw[i] = L.fw;
         fh[i] = L.fh;
@@ -348,6 +343,15 @@ __global__ void __launch_bounds__(kBlock)
     grad_attn[idx] = ga;
     grad_loc[2 * idx] = gx * L.fw;
     grad_loc[2 * idx + 1] = gy * L.fh;
+  }
+}
+
+// Fill with zeros (used before the atomic fallback backward; a kernel rather
+// than a memset so that the launch sequence is graph-capture friendly).
+__global__ void __launch_bounds__(kBlock) zero_kernel(float *x, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    x[i] = 0.0f;
   }
 }
 

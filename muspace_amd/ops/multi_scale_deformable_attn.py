@@ -170,10 +170,9 @@ class _NativeMSDAFunction(torch.autograd.Function):
         value, spatial_shapes, level_start_index, sampling_locations, attention_weights = (
             ctx.saved_tensors
         )
-        # gradients accumulate in float32 whatever the storage dtype; the
-        # kernels overwrite every element of the location/weight gradients,
-        # so only grad_value (scatter-added) needs zeroing
-        grad_value = torch.zeros(value.shape, dtype=torch.float32, device=value.device)
+        # gradients are float32 whatever the storage dtype; the kernels write
+        # every element of all three, so none needs zero-filling
+        grad_value = torch.empty(value.shape, dtype=torch.float32, device=value.device)
         grad_sampling = torch.empty(
             sampling_locations.shape, dtype=torch.float32, device=value.device
         )

@@ -50,6 +50,13 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         + [_c_int64] * 8
         + [_c_ptr],
     ),
+    "ms_deform_attn_backward_ws": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "ms_deform_attn_backward_workspace_size": (ctypes.c_size_t, [_c_int] + [_c_int64] * 7),
 }
 
 
@@ -189,8 +196,9 @@ class NativeLibrary:
     ) -> None:
         """Tensor-level backward with the reference export's argument order.
 
-        grad_value is accumulated into (zero-fill it first); the two other
-        gradient buffers are overwritten.
+        All three gradient buffers are overwritten (none needs zero-filling).
+        The tile-owned kernels' scratch comes from torch's caching allocator
+        on the value's device.
         """
         import torch
 
@@ -221,15 +229,19 @@ class NativeLibrary:
                      tuple(sampling_locations.shape))
         _check_shape(grad_attention_weights, "grad_attention_weights",
                      tuple(attention_weights.shape))
+        nbytes = self._raw["ms_deform_attn_backward_workspace_size"](
+            _dtype_code(value.dtype), batch, spatial, heads, channels, levels, queries, points
+        )
         with torch.cuda.device(value.device):
-            rc = self._raw["ms_deform_attn_backward"](
+            workspace = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=value.device)
+            rc = self._raw["ms_deform_attn_backward_ws"](
                 value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
                 level_start_index.data_ptr(), sampling_locations.data_ptr(),
                 attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
                 grad_output.data_ptr(), grad_value.data_ptr(),
                 grad_sampling_locations.data_ptr(), grad_attention_weights.data_ptr(),
                 batch, spatial, heads, channels, levels, queries, points,
-                int(im2col_step), self._stream(value),
+                int(im2col_step), workspace.data_ptr(), int(nbytes), self._stream(value),
             )
         self._raise_on(rc, "ms_deform_attn_backward")
 

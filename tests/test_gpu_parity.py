@@ -56,8 +56,8 @@ def run_backward(lib, t, grad, value_dtype, geometry_dtype, im2col_step=64):
     loc = t["sampling_locations"].to(geometry_dtype).to(DEV).contiguous()
     attn = t["attention_weights"].to(geometry_dtype).to(DEV).contiguous()
     shapes, starts = t["spatial_shapes"].to(DEV), t["level_start_index"].to(DEV)
-    gv = torch.zeros(value.shape, dtype=torch.float32, device=DEV)
-    # poisoned: every element must be overwritten
+    # poisoned: every element of all three gradients must be overwritten
+    gv = torch.full(value.shape, float("nan"), dtype=torch.float32, device=DEV)
     gl = torch.full(loc.shape, float("nan"), dtype=torch.float32, device=DEV)
     ga = torch.full(attn.shape, float("nan"), dtype=torch.float32, device=DEV)
     lib.ms_deform_attn_backward(value, shapes, starts, loc, attn,
