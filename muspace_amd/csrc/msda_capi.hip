@@ -286,17 +286,22 @@ void launch_backward_atomic(const void *value, const int64_t *shapes, const int6
   }
 }
 
-// Tile edge of the tile-owned backward per channel count (LDS budget of about
-// 72 KB fp32 per workgroup, two workgroups per CU).
-int tile_edge(int channels) { return channels == 64 ? 11 : 16; }
+// Tile edge of the tile-owned backward per channel count (about 150 KB of
+// LDS per workgroup, one 1024-thread workgroup per CU).
+int tile_edge(int channels) {
+  return channels == 16 ? msda::TileEdge<16>::value
+                        : (channels == 32 ? msda::TileEdge<32>::value : msda::TileEdge<64>::value);
+}
 
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 // Scratch layout of the tile-owned backward.
 struct TileWorkspace {
   msda::BinPlan plan;
-  size_t counts, tile_start, gmax, records, bytes;
+  size_t counts, tile_start, records, meta, items, slot_base, multi, partials, bytes;
 };
+
+constexpr size_t kPartialPoolBytes = size_t{256} << 20;  // split-tile partials, all slabs
 
 bool plan_tile_workspace(const msda::Shape &s, TileWorkspace &w) {
   if (s.channels != 16 && s.channels != 32 && s.channels != 64) return false;
@@ -311,21 +316,32 @@ bool plan_tile_workspace(const msda::Shape &s, TileWorkspace &w) {
   p.lp_log2 = log2_int(s.lp > 0 ? s.lp : 1);
   if ((static_cast<int64_t>(s.queries) << p.lp_log2) > (int64_t{1} << 32)) return false;
   p.rec_cap = 4 * static_cast<int64_t>(s.queries) * s.lp;
+  if (p.rec_cap >= (int64_t{1} << 31)) return false;
   const int64_t bm = static_cast<int64_t>(s.batch) * s.heads;
+  const size_t tile_floats = static_cast<size_t>(T) * T * s.channels;
+  p.rmax0 = 2048;
+  int64_t slots = static_cast<int64_t>(kPartialPoolBytes / (bm * tile_floats * 4));
+  p.slot_cap = static_cast<int>(slots < 32 ? 32 : (slots > (1 << 20) ? (1 << 20) : slots));
+  p.item_cap = p.tile_bound + p.slot_cap;
   size_t off = 0;
-  w.counts = off;
-  off = align256(off + static_cast<size_t>(bm) * p.chunks * p.tile_bound * 4);
-  w.tile_start = off;
-  off = align256(off + static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
-  w.gmax = off;
-  off = align256(off + static_cast<size_t>(s.units) * 4);
-  w.records = off;
-  off = align256(off + static_cast<size_t>(bm) * p.rec_cap * 4);
+  auto take = [&off](size_t bytes) {
+    const size_t at = off;
+    off = align256(off + bytes);
+    return at;
+  };
+  w.counts = take(static_cast<size_t>(bm) * p.chunks * p.tile_bound * 4);
+  w.tile_start = take(static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
+  w.records = take(static_cast<size_t>(bm) * p.rec_cap * 4);
+  w.meta = take(static_cast<size_t>(bm) * sizeof(msda::SlabMeta));
+  w.items = take(static_cast<size_t>(bm) * p.item_cap * sizeof(uint2));
+  w.slot_base = take(static_cast<size_t>(bm) * p.tile_bound * 4);
+  w.multi = take(static_cast<size_t>(bm) * p.tile_bound * 4);
+  w.partials = take(static_cast<size_t>(bm) * p.slot_cap * tile_floats * 4);
   w.bytes = off;
   return true;
 }
 
-// Persistent grid of the tile kernel: two workgroups per CU, a multiple of 8
+// Persistent grid of the tile kernel: one workgroup per CU, a multiple of 8
 // (the XCD count) so that every XCD gets the same number of workgroups.
 int tile_grid() {
   static int cached[64] = {0};
@@ -337,7 +353,7 @@ int tile_grid() {
         cus <= 0) {
       cus = 256;
     }
-    cached[dev] = ((2 * cus + 7) / 8) * 8;
+    cached[dev] = ((cus + 7) / 8) * 8;
   }
   return cached[dev];
 }
@@ -347,12 +363,16 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
                            const void *loc, const void *attn, const void *grad_out, float *gv,
                            float *gl, float *ga, const msda::Shape &s, const TileWorkspace &w,
                            void *workspace, hipStream_t st) {
-  constexpr int T = C == 64 ? 11 : 16;
+  constexpr int T = msda::TileEdge<C>::value;
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + w.counts);
   uint32_t *tile_start = reinterpret_cast<uint32_t *>(ws + w.tile_start);
-  float *gmax = reinterpret_cast<float *>(ws + w.gmax);
   uint32_t *records = reinterpret_cast<uint32_t *>(ws + w.records);
+  msda::SlabMeta *meta = reinterpret_cast<msda::SlabMeta *>(ws + w.meta);
+  uint2 *items = reinterpret_cast<uint2 *>(ws + w.items);
+  uint32_t *slot_base = reinterpret_cast<uint32_t *>(ws + w.slot_base);
+  uint32_t *multi = reinterpret_cast<uint32_t *>(ws + w.multi);
+  float *partials = reinterpret_cast<float *>(ws + w.partials);
   const msda::BinPlan &p = w.plan;
   const int bm = s.batch * s.heads;
   const VT *v = static_cast<const VT *>(value);
@@ -361,7 +381,7 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   const VT *go = static_cast<const VT *>(grad_out);
   const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4;
 
-  auto count = msda::msda_bin_count<VT, GT, C, T>;
+  auto count = msda::msda_bin_count<GT, T>;
   auto scatter = msda::msda_bin_scatter<GT, T>;
   auto tile = msda::msda_tile_backward<VT, GT, C, T>;
   const size_t tile_bytes = msda::tile_lds_bytes<T>(C, sizeof(VT));
@@ -372,14 +392,17 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(tile),
                             hipFuncAttributeMaxDynamicSharedMemorySize, tile_bytes);
 
-  count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, go, s, p, counts,
-                                                             gmax, gl, ga);
-  msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(shapes, starts, s, p, counts,
-                                                             tile_start, gv);
+  count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts, gl,
+                                                             ga);
+  msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
+      shapes, starts, s, p, counts, tile_start, meta, items, slot_base, multi, gv);
   scatter<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts,
                                                                records);
-  tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, shapes, starts, lc, aw, go, gmax,
-                                                          records, tile_start, s, p, gv, gl, ga);
+  tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, shapes, starts, lc, aw, go, records,
+                                                          tile_start, meta, items, slot_base, s,
+                                                          p, gv, partials, gl, ga);
+  msda::msda_tile_combine<C, T><<<bm * msda::kCombineBlocksPerSlab, msda::kBinBlock, 0, st>>>(
+      shapes, starts, s, p, tile_start, meta, slot_base, multi, partials, gv);
 }
 
 template <typename VT, typename GT>

@@ -105,6 +105,23 @@ __device__ __forceinline__ void load16(const __half *p, float (&o)[8]) {
   }
 }
 
+// Four channels per lane: 16 bytes of fp32 or 8 bytes of fp16/bf16.
+__device__ __forceinline__ void load4ch(const float *p, float (&o)[4]) { load16(p, o); }
+__device__ __forceinline__ void load4ch(const bf16_t *p, float (&o)[4]) {
+  const uint2 v = *reinterpret_cast<const uint2 *>(p);
+  o[0] = __uint_as_float(v.x << 16);
+  o[1] = __uint_as_float(v.x & 0xffff0000u);
+  o[2] = __uint_as_float(v.y << 16);
+  o[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+__device__ __forceinline__ void load4ch(const __half *p, float (&o)[4]) {
+  const uint2 v = *reinterpret_cast<const uint2 *>(p);
+  o[0] = __half2float(__ushort_as_half(static_cast<unsigned short>(v.x & 0xffffu)));
+  o[1] = __half2float(__ushort_as_half(static_cast<unsigned short>(v.x >> 16)));
+  o[2] = __half2float(__ushort_as_half(static_cast<unsigned short>(v.y & 0xffffu)));
+  o[3] = __half2float(__ushort_as_half(static_cast<unsigned short>(v.y >> 16)));
+}
+
 __device__ __forceinline__ void store16(float *p, const float (&v)[4]) {
   *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
@@ -146,6 +163,18 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (N >= 16) v += MSDA_DPP(v, 0x140); // row_mirror: other half of 16
   if constexpr (N >= 32) v += __shfl_xor(v, 16, kWave);
   if constexpr (N >= 64) v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+// Max over aligned groups of N consecutive lanes, like group_sum.
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (N >= 2) v = fmaxf(v, MSDA_DPP(v, 0xB1));
+  if constexpr (N >= 4) v = fmaxf(v, MSDA_DPP(v, 0x4E));
+  if constexpr (N >= 8) v = fmaxf(v, MSDA_DPP(v, 0x141));
+  if constexpr (N >= 16) v = fmaxf(v, MSDA_DPP(v, 0x140));
+  if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  if constexpr (N >= 64) v = fmaxf(v, __shfl_xor(v, 32, kWave));
   return v;
 }
 
