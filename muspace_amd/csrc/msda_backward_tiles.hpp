@@ -1,63 +1,109 @@
-// Tile-owned MSDA backward for MI355X (gfx950): no global atomics.
+// Tile-owned MSDA backward for MI355X (gfx950).
 //
 // grad_value[b, cell, m, :] = sum over samples s of (b, m) with a bilinear
 // corner at `cell` of  w_corner(s) * attn(s) * grad_out[b, q(s), m, :].
 // The reference scatters this with one fp32 global atomic per corner and
 // channel (ms_deform_attn_musa_kernel.muh:93-166, 625-733). On MI355X, fp32
 // atomics to device memory resolve past the per-XCD L2 (measured ~80-330 G
-// dwords/s), fp32 LDS atomics run at ~0.3 dword/clk/CU and integer LDS
-// atomics stall on bank conflicts, so this path instead makes every output
-// cell the property of one workgroup and accumulates in registers:
+// dwords/s) and fp32 LDS atomics run at ~0.3 dword/clk/CU, so this path makes
+// each value cell the property of one T x T cell tile and accumulates in
+// registers and plain LDS read-modify-writes:
 //
-//   1. bin_count   per (b, m, query chunk): which T x T cell tiles each sample
-//                  touches (up to 4), per-tile histogram in LDS; zero
-//                  location/weight gradients for samples that touch no cell.
+//   1. bin_count   per (b, m, query chunk): the primary tile of every sample
+//                  (the tile holding its clamped top-left corner), per-tile
+//                  histogram in LDS. Also zeroes the gradients of samples
+//                  with no corner inside their level and the tile-boundary
+//                  cells of grad_value (see below).
 //   2. bin_scan    per (b, m): exclusive scan of the histograms -> per-chunk
-//                  write cursors and per-tile record ranges; splits tiles
-//                  with more than `rmax` records into chunks (work items) so
-//                  that a heavily sampled small level is spread over many
-//                  CUs, `rmax` adapted to the partial-tile pool; zeroes value
-//                  rows that belong to no level.
-//   3. bin_scatter per chunk: record id (q << lp_log2 | sample) into its tiles.
-//   4. tile        per work item (persistent, XCD-ordered): stage the value
-//                  tile plus a one-cell halo in LDS, then
-//                  counting-sort its records by top-left corner in LDS and
-//                  let each lane group accumulate, in registers, the four
-//                  corner sums of the positions it owns (no atomics on the
-//                  gradient, see msda_tile_backward); the record whose
-//                  top-left corner lies in the tile also computes grad_attn
-//                  and grad_sampling_loc from the LDS value tile (no value
-//                  gathers from HBM/L2); plain stores to grad_value, or to a
-//                  partial tile when the tile was split.
-//   5. combine     per split tile: sum its partial tiles in chunk order.
-// grad_value and the two other gradients are fully written (no zero-fill).
+//                  write cursors and per-tile record ranges; one work item
+//                  per tile, or several of at most `rmax` records for a tile
+//                  holding more ("split"); items appended, coarsest level
+//                  first, to one compact list; zeroes the cells of empty and
+//                  split tiles and the value rows that belong to no level.
+//   3. bin_scatter per chunk: 16-byte records {query<<lp_log2 | sample,
+//                  location x, location y, attention weight} into their tile.
+//   4. tile        persistent, one 1024-thread workgroup per CU, items taken
+//                  round-robin inside an XCD's share of the list: stage the
+//                  value tile in LDS, then for each batch of K records:
+//                  counting sort by top-left corner position in LDS, stage
+//                  the grad_out rows, and let lane groups own positions and
+//                  accumulate in registers. Records, grad_out rows and the
+//                  next value tile are prefetched one or two batches ahead.
+//
+// Ownership of cells: a record's top-left corner lies on one of the
+// (T+1)^2 positions [-1, T-1]^2 of its primary tile, so its corners cover the
+// cells [0, T]^2 of that tile's frame: the tile's own T x T cells plus a
+// one-cell halo (row T and column T) that belongs to the tiles below and to
+// the right. Cells of a tile's first row (column) also receive halo
+// contributions from the tile above (to the left) unless the tile touches the
+// level's top (left) edge. Those "boundary" cells are zeroed in step 1 and
+// every contribution to them, and to all cells of split tiles, is a line-wide
+// fp32 global atomic add; every other cell gets one plain store.
+// grad_value, grad_sampling_loc and grad_attention_weight are fully written.
 #pragma once
+
+#include <type_traits>
 
 #include "msda_device.hpp"
 
 namespace msda {
 
-constexpr int kTileBlock = 512;          // tile kernel workgroup (8 wavefronts)
+constexpr int kTileBlock = 1024;         // tile kernel workgroup (16 wavefronts)
 constexpr int kBinBlock = 256;           // binning workgroup
 constexpr int kMaxTilesPerSlab = 16384;  // LDS histogram of the binning kernels
-constexpr int kCombineBlocksPerSlab = 16;
+constexpr int kZeroList = 2048;          // tiles listed for zeroing per slab
+constexpr size_t kTileLdsLimit = 160 * 1024;
 
 // Host-computed sizes of the binning scratch (all per (b, m) slab).
 struct BinPlan {
-  int chunks;      // query chunks per slab
-  int chunk_q;     // queries per chunk
-  int tile_bound;  // stride of the per-slab tile arrays (>= tiles per slab)
-  int lp_log2;     // record = (q << lp_log2) | sample
-  int rmax0;       // preferred records per work item
-  int slot_cap;    // partial tiles per slab
-  int item_cap;    // work items per slab (tile_bound + slot_cap)
-  int64_t rec_cap; // record capacity = 4 * queries * lp
+  int chunks;       // query chunks per slab
+  int chunk_q;      // queries per chunk
+  int tile_bound;   // stride of the per-slab tile arrays (>= tiles per slab)
+  int lp_log2;      // record id = (q << lp_log2) | sample
+  int rmax;         // records per work item (a multiple of the batch size)
+  int item_cap;     // capacity of the compact work-item list (all slabs)
+  int64_t rec_cap;  // records per slab = queries * lp (one per sample)
 };
 
-// Per-slab bookkeeping written by bin_scan.
-struct SlabMeta {
-  uint32_t rmax, nitems, nmulti, pad;
+// One work item: records [r0, r1) of one tile of the (b, m) slab. `tile`
+// packs the slab-local tile index (bits 0-15), its level (bits 16-21) and
+// the split flag (bit 31: all cells of the tile are added atomically);
+// (y_lo, x_lo) is the tile origin in its level.
+struct Item {
+  uint32_t b, m, tile, r0;
+  uint32_t r1, y_lo, x_lo, pad;
 };
+constexpr uint32_t kSplitBit = 0x80000000u;
+constexpr uint32_t kTileIndexMask = 0xffffu;
+
+// Tile-kernel configuration per (value type, channels): tile edge T, batch
+// size K (records sorted together) and channels per lane CPL. The LDS holds
+// the value tile with its halo, four fp32 corner planes, K staged grad_out
+// rows, K sorted records, two id buffers and the position counts.
+template <typename VT, int C>
+struct TileCfg;
+template <> struct TileCfg<float, 16> { static constexpr int T = 14, K = 512, CPL = 4; };
+template <> struct TileCfg<float, 32> { static constexpr int T = 10, K = 512, CPL = 4; };
+template <> struct TileCfg<float, 64> { static constexpr int T = 7, K = 256, CPL = 4; };
+template <> struct TileCfg<bf16_t, 16> { static constexpr int T = 14, K = 512, CPL = 4; };
+template <> struct TileCfg<bf16_t, 32> { static constexpr int T = 12, K = 512, CPL = 4; };
+template <> struct TileCfg<bf16_t, 64> { static constexpr int T = 7, K = 512, CPL = 4; };
+template <> struct TileCfg<__half, 16> : TileCfg<bf16_t, 16> {};
+template <> struct TileCfg<__half, 32> : TileCfg<bf16_t, 32> {};
+template <> struct TileCfg<__half, 64> : TileCfg<bf16_t, 64> {};
+
+template <typename VT, int C>
+__host__ __device__ constexpr size_t tile_lds_bytes() {
+  constexpr int T = TileCfg<VT, C>::T, K = TileCfg<VT, C>::K, NPOS = (T + 1) * (T + 1);
+  return static_cast<size_t>(NPOS + 1) * C * sizeof(VT) +  // value tile + halo, zero row
+         static_cast<size_t>(4 * NPOS) * C * 4 +           // corner planes
+         static_cast<size_t>(K) * C * sizeof(VT) +         // staged grad_out rows
+         static_cast<size_t>(K) * 16 +                     // sorted records
+         static_cast<size_t>(2 * K) * 4 +                  // record ids, two batches
+         static_cast<size_t>(3 * NPOS) * 4 +               // position count, offset, order
+         64 * 4 +                                          // count buckets
+         static_cast<size_t>(C) * 4;                       // zero slot
+}
 
 // Per-level tile table in LDS: level l owns tiles [base[l], base[l+1]).
 template <int T>
@@ -73,26 +119,12 @@ __device__ __forceinline__ void stage_tiles(const Level *lv, int levels, int *nt
   __syncthreads();
 }
 
-// Tiles (within the (b, m) slab) holding a valid corner of `t`; the first is
-// the primary tile, which holds corner (max(y0,0), max(x0,0)) and with its
-// halo all four corners. Returns the number of tiles (0 if no valid corner).
+// Primary tile (slab-local index) of a sample with a corner in its level:
+// the tile holding (max(y0, 0), max(x0, 0)).
 template <int T>
-__device__ __forceinline__ int sample_tiles(const Tap &t, int ntc, int base, int (&tiles)[4]) {
-  if (!t.in) return 0;
+__device__ __forceinline__ int primary_tile(const Tap &t, int ntc, int base) {
   const int py = t.y0 < 0 ? 0 : t.y0, px = t.x0 < 0 ? 0 : t.x0;
-  int n = 0;
-  tiles[n++] = base + (py / T) * ntc + px / T;
-  const bool ok[4] = {t.y0ok && t.x0ok, t.y0ok && t.x1ok, t.y1ok && t.x0ok, t.y1ok && t.x1ok};
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    if (!ok[c]) continue;
-    const int y = t.y0 + (c >> 1), x = t.x0 + (c & 1);
-    const int tile = base + (y / T) * ntc + x / T;
-    bool seen = false;
-    for (int i = 0; i < n; ++i) seen |= tiles[i] == tile;
-    if (!seen) tiles[n++] = tile;
-  }
-  return n;
+  return base + (py / T) * ntc + px / T;
 }
 
 // Tile geometry of slab-local tile index tl.
@@ -110,33 +142,66 @@ __device__ __forceinline__ TileGeom tile_geom(int tl, int T, const int *ntc, con
   return g;
 }
 
+__device__ __forceinline__ TileGeom item_geom(const Item &d) {
+  return TileGeom{static_cast<int>((d.tile >> 16) & 63u), static_cast<int>(d.y_lo),
+                  static_cast<int>(d.x_lo)};
+}
+
+// Cell (r, c) of a tile frame (0 <= r, c < T) receives halo contributions
+// from a neighbouring tile.
+__device__ __forceinline__ bool boundary_cell(int r, int c, const TileGeom &g) {
+  return (r == 0 && g.y_lo > 0) || (c == 0 && g.x_lo > 0);
+}
+
+// Zero the C floats of each cell (r, c) in [0, T)^2 of tile g that lies
+// inside the level and satisfies pick(r, c), with `nthreads` threads.
+template <int C, int T, typename Pick>
+__device__ __forceinline__ void zero_tile_cells(float *grad_value, size_t slab, int MC,
+                                                const Level &L, const TileGeom &g, int tid,
+                                                int nthreads, Pick pick) {
+  constexpr int C4 = C / 4;
+  for (int i = tid; i < T * T * C4; i += nthreads) {
+    const int cell = i / C4, c4 = (i % C4) * 4;
+    const int r = cell / T, c = cell % T;
+    const int y = g.y_lo + r, x = g.x_lo + c;
+    if (y >= L.h || x >= L.w || !pick(r, c)) continue;
+    *reinterpret_cast<float4 *>(grad_value + slab +
+                                static_cast<size_t>(L.start + y * L.w + x) * MC + c4) =
+        make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+}
+
 // Block-wide exclusive scan of per-thread run totals (kBinBlock threads);
 // returns this thread's offset, writes the grand total to *total.
 __device__ __forceinline__ uint32_t block_exclusive(uint32_t run, uint32_t *part, uint32_t *total) {
-  part[threadIdx.x] = run;
+  const int lane = threadIdx.x % kWave, wid = threadIdx.x / kWave;
+  uint32_t incl = run;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t up = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += up;
+  }
+  if (lane == kWave - 1) part[wid] = incl;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t acc = 0;
-    for (int i = 0; i < kBinBlock; ++i) {
-      const uint32_t v = part[i];
-      part[i] = acc;
-      acc += v;
-    }
-    *total = acc;
+  uint32_t before = 0, all = 0;
+  for (int w = 0; w < kBinBlock / kWave; ++w) {
+    const uint32_t v = part[w];
+    before += w < wid ? v : 0u;
+    all += v;
   }
   __syncthreads();
-  const uint32_t off = part[threadIdx.x];
-  __syncthreads();
-  return off;
+  *total = all;
+  return before + incl - run;
 }
 
 // ------------------------------------------------------------ 1. count ---
 
-template <typename GT, int T>
+template <typename GT, int C, int T>
 __global__ void __launch_bounds__(kBinBlock)
     msda_bin_count(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                    const GT *__restrict__ loc, Shape s, BinPlan p,
-                   uint32_t *__restrict__ counts, float *__restrict__ grad_loc,
+                   uint32_t *__restrict__ counts, uint32_t *__restrict__ item_total,
+                   float *__restrict__ grad_value, float *__restrict__ grad_loc,
                    float *__restrict__ grad_attn) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
@@ -145,6 +210,7 @@ __global__ void __launch_bounds__(kBinBlock)
   stage_tiles<T>(lv, s.levels, ntc, base);
   const int nt = base[s.levels];
   for (int i = threadIdx.x; i < nt; i += blockDim.x) hist[i] = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *item_total = 0;
   __syncthreads();
 
   const int bm = blockIdx.x / p.chunks, ch = blockIdx.x % p.chunks;
@@ -160,14 +226,21 @@ __global__ void __launch_bounds__(kBinBlock)
     const size_t o = (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp;
     const int l = level_of_sample(smp, s);
     const Tap t = make_tap(to_float(loc[2 * o]), to_float(loc[2 * o + 1]), lv[l], true);
-    int tiles[4];
-    const int n = sample_tiles<T>(t, ntc[l], base[l], tiles);
-    if (n == 0) {
+    if (!t.in) {
       grad_attn[o] = 0.0f;
-      grad_loc[2 * o] = 0.0f;
-      grad_loc[2 * o + 1] = 0.0f;
+      *reinterpret_cast<float2 *>(grad_loc + 2 * o) = make_float2(0.0f, 0.0f);
+      continue;
     }
-    for (int j = 0; j < n; ++j) atomicAdd(&hist[tiles[j]], 1u);
+    atomicAdd(&hist[primary_tile<T>(t, ntc[l], base[l])], 1u);
+  }
+
+  // boundary cells of the slab's tiles ch, ch + chunks, ...
+  const int MC = s.heads * C;
+  const size_t slab = static_cast<size_t>(b) * s.spatial * MC + m * C;
+  for (int tl = ch; tl < nt; tl += p.chunks) {
+    const TileGeom g = tile_geom(tl, T, ntc, base);
+    zero_tile_cells<C, T>(grad_value, slab, MC, lv[g.l], g, threadIdx.x, blockDim.x,
+                          [&](int r, int c) { return boundary_cell(r, c, g); });
   }
   __syncthreads();
   uint32_t *row = counts + static_cast<size_t>(blockIdx.x) * p.tile_bound;
@@ -180,22 +253,21 @@ template <int C, int T>
 __global__ void __launch_bounds__(kBinBlock)
     msda_bin_scan(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                   Shape s, BinPlan p, uint32_t *__restrict__ counts,
-                  uint32_t *__restrict__ tile_start, SlabMeta *__restrict__ meta,
-                  uint2 *__restrict__ items, uint32_t *__restrict__ slot_base,
-                  uint32_t *__restrict__ multi, float *__restrict__ grad_value) {
+                  uint32_t *__restrict__ tile_start, uint32_t *__restrict__ item_total,
+                  Item *__restrict__ items, float *__restrict__ grad_value) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
-  __shared__ uint32_t part[kBinBlock];
-  __shared__ uint32_t total;
+  __shared__ uint32_t part[kBinBlock / kWave];
+  __shared__ uint32_t item_base, zero_count;
+  __shared__ uint32_t zero_list[kZeroList];
   stage_levels(lv, shapes, starts, s);
   stage_tiles<T>(lv, s.levels, ntc, base);
   const int nt = base[s.levels];
   const int bm = blockIdx.x;
+  const int b = bm / s.heads, m = bm % s.heads;
   uint32_t *cnt = counts + static_cast<size_t>(bm) * p.chunks * p.tile_bound;
   uint32_t *ts = tile_start + static_cast<size_t>(bm) * (p.tile_bound + 1);
-  uint2 *it = items + static_cast<size_t>(bm) * p.item_cap;
-  uint32_t *sb = slot_base + static_cast<size_t>(bm) * p.tile_bound;
-  uint32_t *mu = multi + static_cast<size_t>(bm) * p.tile_bound;
+  if (threadIdx.x == 0) zero_count = 0;
 
   // each thread owns a contiguous run of tiles
   const int per = (nt + kBinBlock - 1) / kBinBlock;
@@ -207,10 +279,11 @@ __global__ void __launch_bounds__(kBinBlock)
     ts[t] = tot;  // the tile's record count until it is replaced by its offset
     run += tot;
   }
+  uint32_t total;
   uint32_t off = block_exclusive(run, part, &total);
   if (threadIdx.x == 0) ts[nt] = total;
   for (int t = t0; t < t1; ++t) {
-    const uint32_t tot = ts[t];
+    const uint32_t n = ts[t];
     ts[t] = off;
     uint32_t cur = off;
     for (int c = 0; c < p.chunks; ++c) {
@@ -219,73 +292,77 @@ __global__ void __launch_bounds__(kBinBlock)
       *x = cur;
       cur += v;
     }
-    off += tot;
+    off += n;
   }
   __syncthreads();
 
-  // records per work item: the smallest rmax >= rmax0 whose split tiles fit
-  // the slab's partial-tile pool
-  uint32_t rmax = static_cast<uint32_t>(p.rmax0);
-  for (;;) {
-    uint32_t need = 0;
-    for (int t = t0; t < t1; ++t) {
-      const uint32_t n = ts[t + 1] - ts[t];
-      if (n > rmax) need += (n + rmax - 1) / rmax;
-    }
-    uint32_t slots;
-    block_exclusive(need, part, &total);
-    slots = total;
-    __syncthreads();
-    if (slots <= static_cast<uint32_t>(p.slot_cap) || rmax >= (1u << 31)) break;
-    rmax *= 2;
+  // items, tiles in reverse order (coarse, densely sampled levels first);
+  // thread i owns reversed positions [u0, u1)
+  const uint32_t rmax = static_cast<uint32_t>(p.rmax);
+  const int u0 = t0, u1 = t1;
+  uint32_t r_items = 0;
+  for (int u = u0; u < u1; ++u) {
+    const int t = nt - 1 - u;
+    r_items += (ts[t + 1] - ts[t] + rmax - 1) / rmax;
   }
+  uint32_t slab_items;
+  uint32_t item_off = block_exclusive(r_items, part, &slab_items);
+  if (threadIdx.x == 0) item_base = atomicAdd(item_total, slab_items);
+  __syncthreads();
+  item_off += item_base;
+  for (int u = u0; u < u1; ++u) {
+    const int t = nt - 1 - u;
+    const uint32_t a = ts[t], e = ts[t + 1], n = e - a;
+    const uint32_t k = (n + rmax - 1) / rmax;
+    if (k != 1) {
+      const uint32_t z = atomicAdd(&zero_count, 1u);
+      if (z < static_cast<uint32_t>(kZeroList)) zero_list[z] = static_cast<uint32_t>(t);
+    }
+    const TileGeom g = k > 0 ? tile_geom(t, T, ntc, base) : TileGeom{0, 0, 0};
+    for (uint32_t j = 0; j < k; ++j) {
+      Item it;
+      it.b = static_cast<uint32_t>(b);
+      it.m = static_cast<uint32_t>(m);
+      it.tile = static_cast<uint32_t>(t) | (static_cast<uint32_t>(g.l) << 16) |
+                (k > 1 ? kSplitBit : 0u);
+      it.r0 = a + j * rmax;
+      it.r1 = min(e, it.r0 + rmax);
+      it.y_lo = static_cast<uint32_t>(g.y_lo);
+      it.x_lo = static_cast<uint32_t>(g.x_lo);
+      it.pad = 0;
+      if (item_off < static_cast<uint32_t>(p.item_cap)) items[item_off] = it;
+      ++item_off;
+    }
+  }
+  __syncthreads();
 
-  // work items, partial slots and the list of split tiles
-  uint32_t n_items = 0, n_slots = 0, n_multi = 0;
-  for (int t = t0; t < t1; ++t) {
-    const uint32_t n = ts[t + 1] - ts[t];
-    const uint32_t c = n > rmax ? (n + rmax - 1) / rmax : 1;
-    n_items += c;
-    if (c > 1) {
-      n_slots += c;
-      n_multi += 1;
+  // non-boundary cells of empty and split tiles (boundary cells: bin_count)
+  const int MC = s.heads * C;
+  const size_t slab = static_cast<size_t>(b) * s.spatial * MC + m * C;
+  const uint32_t nz = zero_count;
+  const bool listed = nz <= static_cast<uint32_t>(kZeroList);
+  for (uint32_t i = 0; i < (listed ? nz : static_cast<uint32_t>(nt)); ++i) {
+    const int t = listed ? static_cast<int>(zero_list[i]) : static_cast<int>(i);
+    if (!listed) {
+      const uint32_t n = ts[t + 1] - ts[t];
+      if (n != 0 && n <= rmax) continue;
     }
-  }
-  uint32_t item_off = block_exclusive(n_items, part, &total);
-  const uint32_t items_total = total;
-  uint32_t slot_off = block_exclusive(n_slots, part, &total);
-  uint32_t multi_off = block_exclusive(n_multi, part, &total);
-  const uint32_t multi_total = total;
-  for (int t = t0; t < t1; ++t) {
-    const uint32_t n = ts[t + 1] - ts[t];
-    const uint32_t c = n > rmax ? (n + rmax - 1) / rmax : 1;
-    for (uint32_t k = 0; k < c; ++k) it[item_off + k] = make_uint2(t, k);
-    item_off += c;
-    if (c > 1) {
-      sb[t] = slot_off;
-      slot_off += c;
-      mu[multi_off++] = t;
-    }
-  }
-  if (threadIdx.x == 0) {
-    SlabMeta mt;
-    mt.rmax = rmax;
-    mt.nitems = items_total;
-    mt.nmulti = multi_total;
-    mt.pad = 0;
-    meta[bm] = mt;
+    const TileGeom g = tile_geom(t, T, ntc, base);
+    zero_tile_cells<C, T>(grad_value, slab, MC, lv[g.l], g, threadIdx.x, blockDim.x,
+                          [&](int r, int c) { return !boundary_cell(r, c, g); });
   }
 
   // value rows of this (b, m) that belong to no level get a zero gradient
-  const int b = bm / s.heads, m = bm % s.heads;
   for (int cell = threadIdx.x; cell < s.spatial; cell += blockDim.x) {
     bool covered = false;
     for (int l = 0; l < s.levels && !covered; ++l) {
       covered = cell >= lv[l].start && cell < lv[l].start + lv[l].h * lv[l].w;
     }
     if (!covered) {
-      float *row = grad_value + (static_cast<size_t>(b) * s.spatial + cell) * s.heads * C + m * C;
-      for (int c = 0; c < C; ++c) row[c] = 0.0f;
+      float *row = grad_value + slab + static_cast<size_t>(cell) * MC;
+      for (int c = 0; c < C; c += 4) {
+        *reinterpret_cast<float4 *>(row + c) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
     }
   }
 }
@@ -295,8 +372,8 @@ __global__ void __launch_bounds__(kBinBlock)
 template <typename GT, int T>
 __global__ void __launch_bounds__(kBinBlock)
     msda_bin_scatter(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
-                     const GT *__restrict__ loc, Shape s, BinPlan p,
-                     const uint32_t *__restrict__ counts, uint32_t *__restrict__ records) {
+                     const GT *__restrict__ loc, const GT *__restrict__ attn, Shape s, BinPlan p,
+                     const uint32_t *__restrict__ counts, uint4 *__restrict__ records) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
   extern __shared__ uint32_t cursor[];
@@ -311,367 +388,435 @@ __global__ void __launch_bounds__(kBinBlock)
   const int b = bm / s.heads, m = bm % s.heads;
   const int q0 = ch * p.chunk_q;
   const int nq = min(p.chunk_q, s.queries - q0);
-  uint32_t *rec = records + static_cast<size_t>(bm) * p.rec_cap;
+  uint4 *rec = records + static_cast<size_t>(bm) * p.rec_cap;
   const int lpp = 1 << p.lp_log2;
   for (int i = threadIdx.x; i < nq * lpp; i += blockDim.x) {
     const int q = q0 + (i >> p.lp_log2), smp = i & (lpp - 1);
     if (smp >= s.lp) continue;
     const size_t o = (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp;
     const int l = level_of_sample(smp, s);
-    const Tap t = make_tap(to_float(loc[2 * o]), to_float(loc[2 * o + 1]), lv[l], true);
-    int tiles[4];
-    const int n = sample_tiles<T>(t, ntc[l], base[l], tiles);
+    const float lx = to_float(loc[2 * o]), ly = to_float(loc[2 * o + 1]);
+    const Tap t = make_tap(lx, ly, lv[l], true);
+    if (!t.in) continue;
     const uint32_t id = (static_cast<uint32_t>(q) << p.lp_log2) | static_cast<uint32_t>(smp);
-    for (int j = 0; j < n; ++j) rec[atomicAdd(&cursor[tiles[j]], 1u)] = id;
+    const uint32_t at = atomicAdd(&cursor[primary_tile<T>(t, ntc[l], base[l])], 1u);
+    rec[at] = make_uint4(id, __float_as_uint(lx), __float_as_uint(ly),
+                         __float_as_uint(to_float(attn[o])));
   }
 }
 
 // ------------------------------------------------------------- 4. tile ---
 
-// Tile edge per channel count: four fp32 corner planes of T*T cells, the
-// value tile with its halo and the record stash fill about 150 KB of LDS.
-template <int C>
-struct TileEdge {
-  static constexpr int value = C == 16 ? 15 : (C == 32 ? 14 : 10);
+// Position in one workgroup's batch sequence: item n of its round-robin
+// share, batch k of that item, and the item's descriptor.
+struct BatchCursor {
+  int n;
+  uint32_t k;
+  Item d;
+  bool valid;
 };
 
-constexpr int kStash = 1024;  // records sorted per sub-batch
-
-template <int T>
-__host__ __device__ constexpr size_t tile_lds_bytes(int c, int value_bytes) {
-  return static_cast<size_t>((T + 1) * (T + 1)) * c * value_bytes +  // value tile + halo
-         static_cast<size_t>(4 * T * T) * c * 4 +                   // corner planes (fp32)
-         static_cast<size_t>(kStash) * 16 +                         // sorted record stash
-         static_cast<size_t>((T + 1) * (T + 1)) * 8;                // position count, offset
+template <int K>
+__device__ __forceinline__ uint32_t item_batches(const Item &d) {
+  return (d.r1 - d.r0 + K - 1) / K;
 }
 
-// One work item = a tile of T x T value cells and a range of its records.
-// Every record's top-left corner lies on one of the (T+1)^2 positions
-// [-1, T-1]^2 around the tile. Records are counting-sorted by position in
-// LDS; a lane group owns positions and accumulates, in registers, the four
-// corner sums S_p[d] = sum_r w_d(r) * attn(r) * grad_out[q(r)] of its
-// positions; each S_p[d] then lands on cell p + d of corner plane d, a cell
-// that no other position writes, and the planes are summed per cell. No
-// atomic touches the gradient. A record whose top-left corner (clamped to the
-// level) is inside the tile is its primary record and also produces the
-// attention-weight and location gradients from the LDS value tile.
-template <typename VT, typename GT, int C, int T>
+// One work item = records [r0, r1) of a tile of T x T value cells. The
+// records are processed in batches of K: counting-sorted by top-left corner
+// position ((T+1)^2 positions, [-1, T-1]^2 in the tile frame), then lane
+// group g owns positions g, g + NG, ... and accumulates, in registers, the
+// four corner sums S_p[d] = sum_r w_d(r) * attn(r) * grad_out[q(r)] of each
+// of them; S_p[d] is added to slot p of corner plane d (no other group writes
+// it). At the end of the item, cell (r, c) sums slot (r - dy, c - dx) of
+// plane (dy, dx). Per record, the owner group also produces the attention
+// and location gradients from the LDS value tile:
+//   D_d = grad_out . v_d (corner value rows), grad_attn = sum_d w_d D_d,
+//   grad_ix = attn * (wy0 (D1 - D0) + wy1 (D3 - D2)),
+//   grad_iy = attn * (wx0 (D2 - D0) + wx1 (D3 - D1)),
+//   grad_loc = (grad_ix * W, grad_iy * H)   (d ix / d loc_x = W)
+// which is grid_sample's bilinear backward (zeros padding) regrouped by
+// corner.
+template <typename VT, int C>
 __global__ void __launch_bounds__(kTileBlock)
     msda_tile_backward(const VT *__restrict__ value, const int64_t *__restrict__ shapes,
-                       const int64_t *__restrict__ starts, const GT *__restrict__ loc,
-                       const GT *__restrict__ attn, const VT *__restrict__ grad_out,
-                       const uint32_t *__restrict__ records,
-                       const uint32_t *__restrict__ tile_start,
-                       const SlabMeta *__restrict__ meta, const uint2 *__restrict__ items,
-                       const uint32_t *__restrict__ slot_base, Shape s, BinPlan p,
-                       float *__restrict__ grad_value, float *__restrict__ partials,
-                       float *__restrict__ grad_loc, float *__restrict__ grad_attn) {
-  // four channels per lane whatever the storage type, so that the per-lane
-  // accumulators fit the register budget of 1024-thread workgroups
-  constexpr int CPL = 4, KQ = C / CPL, TV = T + 1, NPOS = TV * TV;
-  constexpr int UPC = C * static_cast<int>(sizeof(VT)) / 16;  // 16-byte units per value row
-  constexpr int NGROUPS = kTileBlock / KQ;
-  constexpr int PPG = (NPOS + NGROUPS - 1) / NGROUPS;  // positions per lane group
-  static_assert(C % CPL == 0 && (KQ & (KQ - 1)) == 0 && KQ <= kWave, "bad tile layout");
+                       const int64_t *__restrict__ starts, const VT *__restrict__ grad_out,
+                       const uint4 *__restrict__ records, const Item *__restrict__ items,
+                       const uint32_t *__restrict__ item_total, Shape s, BinPlan p,
+                       float *__restrict__ grad_value, float *__restrict__ grad_loc,
+                       float *__restrict__ grad_attn) {
+  using Cfg = TileCfg<VT, C>;
+  constexpr int T = Cfg::T, K = Cfg::K, CPL = Cfg::CPL;
+  constexpr int TV = T + 1, NPOS = TV * TV;
+  constexpr int KQ = C / CPL;          // lanes per group
+  constexpr int NG = kTileBlock / KQ;  // lane groups
+  constexpr int GROWS = K / NG;        // grad_out rows staged per group and batch
+  constexpr int VB = static_cast<int>(sizeof(VT));
+  constexpr int UPV = C * VB / 16;     // 16-byte units per value row
+  constexpr int LANE_B = CPL * VB;     // bytes per lane and grad_out row
+  // native vector types (HIP's uint4 is a union wrapper that keeps arrays of
+  // it in scratch memory)
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  using LaneUnit = typename std::conditional<LANE_B == 16, u32x4, u32x2>::type;
+  static_assert(CPL == 4 && (KQ & (KQ - 1)) == 0 && KQ <= kWave, "bad lane layout");
+  static_assert(NPOS * UPV <= kTileBlock, "value tile: one 16-byte unit per thread");
+  static_assert(K <= kTileBlock && K % NG == 0 && NPOS <= kTileBlock, "bad batch size");
+  static_assert(tile_lds_bytes<VT, C>() + 3400 <= kTileLdsLimit, "tile LDS budget");
+
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
   extern __shared__ __align__(16) unsigned char lds[];
-  VT *vt = reinterpret_cast<VT *>(lds);
-  float *planes = reinterpret_cast<float *>(lds + static_cast<size_t>(NPOS) * C * sizeof(VT));
-  uint4 *stash = reinterpret_cast<uint4 *>(planes + 4 * T * T * C);
-  uint32_t *pcount = reinterpret_cast<uint32_t *>(stash + kStash);
+  VT *vt = reinterpret_cast<VT *>(lds);  // NPOS cells + one zero row
+  float *planes = reinterpret_cast<float *>(lds + static_cast<size_t>(NPOS + 1) * C * VB);
+  VT *gst = reinterpret_cast<VT *>(planes + 4 * NPOS * C);
+  uint4 *stash = reinterpret_cast<uint4 *>(gst + K * C);
+  uint32_t *ids = reinterpret_cast<uint32_t *>(stash + K);  // [2][K]
+  uint32_t *pcount = ids + 2 * K;
   uint32_t *poff = pcount + NPOS;
+  uint32_t *order = poff + NPOS;
+  uint32_t *bucket = order + NPOS;                         // [64]
+  float *dummy = reinterpret_cast<float *>(bucket + 64);  // [C], always zero
 
   stage_levels(lv, shapes, starts, s);
   stage_tiles<T>(lv, s.levels, ntc, base);
   const int MC = s.heads * C;
+  const int tid = threadIdx.x;
+  const int grp = tid / KQ, k = tid % KQ;
 
+  // this workgroup's items: lo + wid, lo + wid + nw, ... below hi
   constexpr int kXcd = 8;
-  const int xcd = blockIdx.x % kXcd, per_xcd = gridDim.x / kXcd;
-  const int64_t total = static_cast<int64_t>(s.batch) * s.heads * p.item_cap;
-  const int64_t lo = total * xcd / kXcd, hi = total * (xcd + 1) / kXcd;
-  const int grp = threadIdx.x / KQ, k = threadIdx.x % KQ;
+  const uint32_t n_items = min(*item_total, static_cast<uint32_t>(p.item_cap));
+  const int xcd = blockIdx.x % kXcd, wid = blockIdx.x / kXcd, nw = gridDim.x / kXcd;
+  const uint32_t lo = static_cast<uint32_t>(static_cast<uint64_t>(n_items) * xcd / kXcd);
+  const uint32_t hi = static_cast<uint32_t>(static_cast<uint64_t>(n_items) * (xcd + 1) / kXcd);
+  auto item_at = [&](int n, bool &ok) {
+    const uint64_t idx = static_cast<uint64_t>(lo) + wid + static_cast<uint64_t>(n) * nw;
+    ok = idx < hi;
+    Item d{0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    if (ok) d = items[idx];
+    return d;
+  };
+
+  // cursors of batches b (c0), b + 1 (c1) and b + 2 (c2); `pre` is the
+  // descriptor of the item after c2's
+  BatchCursor c0;
+  c0.n = 0;
+  c0.k = 0;
+  c0.d = item_at(0, c0.valid);
+  if (!c0.valid) return;  // uniform: no item for this workgroup
+  bool pre_ok;
+  Item pre = item_at(1, pre_ok);
+  auto advance = [&](const BatchCursor &c) {
+    BatchCursor r = c;
+    if (!c.valid) return r;
+    if (c.k + 1 < item_batches<K>(c.d)) {
+      r.k = c.k + 1;
+    } else {
+      r.n = c.n + 1;
+      r.k = 0;
+      r.d = pre;
+      r.valid = pre_ok;
+      pre = item_at(r.n + 1, pre_ok);
+    }
+    return r;
+  };
+  BatchCursor c1 = advance(c0);
+  BatchCursor c2 = advance(c1);
+
+  auto batch_range = [&](const BatchCursor &c, uint32_t &s0, uint32_t &s1) {
+    s0 = c.d.r0 + c.k * K;
+    s1 = min(c.d.r1, s0 + K);
+  };
+  // Loads below are issued unconditionally (a clamped, always valid address
+  // when there is nothing to load) so that no branch separates a prefetch
+  // from the code that consumes it a batch later.
+  auto load_record = [&](const BatchCursor &c) {
+    uint32_t s0, s1;
+    batch_range(c, s0, s1);
+    const bool ok = c.valid && tid < K && s0 + tid < s1;
+    const size_t at =
+        ok ? static_cast<size_t>(c.d.b * s.heads + c.d.m) * p.rec_cap + s0 + tid : 0;
+    return records[at];
+  };
+  auto geom = [&](const BatchCursor &c) {
+    return item_geom(c.d);
+  };
+  auto slab_offset = [&](const Item &d) {
+    return static_cast<size_t>(d.b) * s.spatial * MC + d.m * C;
+  };
+  // source of this thread's 16-byte unit of the value tile (cells [0, T]^2)
+  // of c's item; `ok` false for cells outside the level (stored as zeros)
+  auto value_unit_src = [&](const BatchCursor &c, bool &ok) {
+    const TileGeom g = geom(c);
+    const Level L = lv[g.l];
+    const int u = tid < NPOS * UPV ? tid : 0;
+    const int cell = u / UPV, kk = u % UPV;
+    const int y = g.y_lo + cell / TV, x = g.x_lo + cell % TV;
+    ok = c.valid && tid < NPOS * UPV && y < L.h && x < L.w;
+    const size_t at =
+        ok ? slab_offset(c.d) + static_cast<size_t>(L.start + y * L.w + x) * MC : 0;
+    return reinterpret_cast<const uint4 *>(value + at) + (ok ? kk : 0);
+  };
+  // source of row grp + j * NG of c's batch of grad_out rows, in record
+  // order (record ids read from bid; rows past the batch read row 0)
+  auto grow_src = [&](const BatchCursor &c, const uint32_t *bid, int j) {
+    uint32_t s0, s1;
+    batch_range(c, s0, s1);
+    const int ns = c.valid ? static_cast<int>(s1 - s0) : 0;
+    const int b = static_cast<int>(c.d.b), m = static_cast<int>(c.d.m);
+    const int t = grp + j * NG;
+    const int q = t < ns ? static_cast<int>(bid[t] >> p.lp_log2) : 0;
+    return reinterpret_cast<const LaneUnit *>(
+        grad_out + ((static_cast<size_t>(b) * s.queries + q) * s.heads + m) * C + k * CPL);
+  };
   const uint32_t smask = (1u << p.lp_log2) - 1u;
-
-  for (int64_t flat = lo + blockIdx.x / kXcd; flat < hi; flat += per_xcd) {
-    const int bm = static_cast<int>(flat / p.item_cap);
-    const int j = static_cast<int>(flat % p.item_cap);
-    const SlabMeta mt = meta[bm];
-    if (static_cast<uint32_t>(j) >= mt.nitems) continue;  // uniform across the block
-    const uint2 item = items[static_cast<size_t>(bm) * p.item_cap + j];
-    const int tl = static_cast<int>(item.x);
-    const int b = bm / s.heads, m = bm % s.heads;
-    const TileGeom tg = tile_geom(tl, T, ntc, base);
-    const Level L = lv[tg.l];
-    const int y_lo = tg.y_lo, x_lo = tg.x_lo;
-    const size_t slab = static_cast<size_t>(b) * s.spatial * MC + m * C;
-    const uint32_t *ts = tile_start + static_cast<size_t>(bm) * (p.tile_bound + 1);
-    const uint32_t t_r0 = ts[tl], t_r1 = ts[tl + 1];
-    const bool split = t_r1 - t_r0 > mt.rmax;
-    const uint32_t r0 = t_r0 + item.y * mt.rmax;
-    const uint32_t r1 = min(t_r1, r0 + mt.rmax);
-    const uint32_t *rec = records + static_cast<size_t>(bm) * p.rec_cap;
-
-    // stage the value tile (rows y_lo..y_lo+T, cols x_lo..x_lo+T)
-    for (int i = threadIdx.x; i < NPOS * UPC; i += kTileBlock) {
-      const int cell = i / UPC, kk = i % UPC;
-      const int r = cell / TV, c = cell % TV;
-      if (y_lo + r < L.h && x_lo + c < L.w) {
-        const VT *src = value + slab +
-                        static_cast<size_t>(L.start + (y_lo + r) * L.w + x_lo + c) * MC;
-        reinterpret_cast<uint4 *>(vt + cell * C)[kk] = reinterpret_cast<const uint4 *>(src)[kk];
+  // location and weight gradients of sorted record j of a finished batch:
+  // stash[j] = {t, wx1, wy1, attn}, the owner left D_0..D_3 at the start of
+  // grad_out row t, bid = the batch's record ids
+  auto finish_record = [&](int j, const uint32_t *bid, const Item &d, const Level &Lf,
+                           uint32_t &o, float &ga, float &gx, float &gy) {
+    const uint4 e = stash[j];
+    const int t = static_cast<int>(e.x);
+    const float4 D = *reinterpret_cast<const float4 *>(gst + t * C);
+    const float wx1 = __uint_as_float(e.y), wy1 = __uint_as_float(e.z);
+    const float a = __uint_as_float(e.w);
+    const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
+    const uint32_t id = bid[t];
+    const int b = static_cast<int>(d.b), m = static_cast<int>(d.m);
+    const int q = static_cast<int>(id >> p.lp_log2), smp = static_cast<int>(id & smask);
+    o = static_cast<uint32_t>(((static_cast<size_t>(b) * s.queries + q) * s.heads + m) * s.lp +
+                              smp);
+    ga = wy0 * (wx0 * D.x + wx1 * D.y) + wy1 * (wx0 * D.z + wx1 * D.w);
+    gx = a * (wy0 * (D.y - D.x) + wy1 * (D.w - D.z)) * Lf.fw;
+    gy = a * (wx0 * (D.z - D.x) + wx1 * (D.w - D.y)) * Lf.fh;
+  };
+  // cell sums of a finished item's corner planes to grad_value; every plane
+  // slot that maps to a cell of [0, T]^2 is read once and zeroed (slots that
+  // map to row or column -1 only ever hold contributions of invalid corners)
+  auto write_back = [&](const Item &d) {
+    const TileGeom g = item_geom(d);
+    const Level Lw = lv[g.l];
+    const bool split = (d.tile & kSplitBit) != 0;
+    const size_t slab = slab_offset(d);
+    for (int i = tid; i < NPOS * C; i += kTileBlock) {
+      const int cell = i / C, ch = i % C;
+      const int r = cell / TV, c = cell % TV;  // cell (r, c) of [0, T]^2
+      float sum = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int pr = r - (q >> 1), pc = c - (q & 1);  // position, >= -1
+        float *pl = pr < T && pc < T ? planes + (q * NPOS + (pr + 1) * TV + pc + 1) * C + ch
+                                     : dummy + ch;  // always zero
+        sum += *pl;
+        *pl = 0.0f;
+      }
+      const int y = g.y_lo + r, x = g.x_lo + c;
+      if (y >= Lw.h || x >= Lw.w) continue;
+      float *dst = grad_value + slab + static_cast<size_t>(Lw.start + y * Lw.w + x) * MC + ch;
+      if (!split && r < T && c < T && !boundary_cell(r, c, g)) {
+        *dst = sum;
+      } else {
+        unsafeAtomicAdd(dst, sum);
       }
     }
+  };
 
-    for (int i = threadIdx.x; i < T * T * C; i += kTileBlock) {
-      *reinterpret_cast<float4 *>(planes + 4 * i) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  // prologue: batch 0's records, value tile and grad_out rows
+  uint4 r_cur = load_record(c0);
+  uint4 r_next = load_record(c1);
+  {
+    bool ok0;
+    const uint4 u = *value_unit_src(c0, ok0);
+    if (tid < NPOS * UPV) {
+      reinterpret_cast<uint4 *>(vt)[tid] = ok0 ? u : make_uint4(0u, 0u, 0u, 0u);
     }
+  }
+  if (tid < UPV) reinterpret_cast<uint4 *>(vt + NPOS * C)[tid] = make_uint4(0u, 0u, 0u, 0u);
+  if (tid < C) dummy[tid] = 0.0f;
+  for (int i = tid; i < NPOS * C; i += kTileBlock) {
+    reinterpret_cast<float4 *>(planes)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  if (tid < NPOS) pcount[tid] = 0;
+  if (tid < K) ids[tid] = r_cur.x;
+  __syncthreads();
+  LaneUnit gregs[GROWS];
+#pragma unroll
+  for (int j = 0; j < GROWS; ++j) gregs[j] = *grow_src(c0, ids, j);
 
-    for (uint32_t sb0 = r0; sb0 < r1; sb0 += kStash) {
-      const uint32_t sb1 = min(r1, sb0 + kStash);
-      for (int i = threadIdx.x; i < NPOS; i += kTileBlock) pcount[i] = 0;
-      __syncthreads();
-      // sort phase: position and rank of each record of the sub-batch
-      uint4 entry[kStash / kTileBlock];
-      int pos[kStash / kTileBlock];
-      uint32_t rank[kStash / kTileBlock];
-#pragma unroll
-      for (int u = 0; u < kStash / kTileBlock; ++u) {
-        const uint32_t i = sb0 + u * kTileBlock + threadIdx.x;
-        pos[u] = -1;
-        if (i >= sb1) continue;
-        const uint32_t id = rec[i];
-        const int q = static_cast<int>(id >> p.lp_log2), smp = static_cast<int>(id & smask);
-        if (q >= s.queries || smp >= s.lp) continue;  // never true for records bin_scatter wrote
-        const size_t si = (static_cast<size_t>(b) * s.queries + q) * s.heads + m;
-        const size_t o = si * s.lp + smp;
-        const Tap t = make_tap(to_float(loc[2 * o]), to_float(loc[2 * o + 1]), L, true);
-        const int py = t.y0 - y_lo + 1, px = t.x0 - x_lo + 1;
-        if (!t.in || py < 0 || py >= TV || px < 0 || px >= TV) continue;  // likewise never
-        pos[u] = py * TV + px;
-        entry[u] = make_uint4(id, __float_as_uint(t.wx1), __float_as_uint(t.wy1),
-                              __float_as_uint(to_float(attn[o])));
-        rank[u] = atomicAdd(&pcount[pos[u]], 1u);
-      }
-      __syncthreads();
-      if (threadIdx.x < kWave) {
-        // exclusive scan of the position counts by one wavefront
-        uint32_t carry = 0;
-        for (int c0 = 0; c0 < NPOS; c0 += kWave) {
-          const int c = c0 + static_cast<int>(threadIdx.x);
-          const uint32_t v = c < NPOS ? pcount[c] : 0u;
-          uint32_t incl = v;
-#pragma unroll
-          for (int d = 1; d < kWave; d <<= 1) {
-            const uint32_t up = __shfl_up(incl, d, kWave);
-            if (static_cast<int>(threadIdx.x) >= d) incl += up;
-          }
-          if (c < NPOS) poff[c] = carry + incl - v;
-          carry += __shfl(incl, kWave - 1, kWave);
-        }
-      }
-      __syncthreads();
-#pragma unroll
-      for (int u = 0; u < kStash / kTileBlock; ++u) {
-        if (pos[u] >= 0) stash[poff[pos[u]] + rank[u]] = entry[u];
-      }
-      __syncthreads();
+  int ns_prev = 0;        // records of the previous batch (gradients pending)
+  uint32_t f_o = 0;       // this thread's pending location/weight gradients
+  float f_ga = 0.0f, f_gx = 0.0f, f_gy = 0.0f;
+  bool wb_pending = false;  // the previous batch finished an item
+  Item wb_item{0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  for (uint32_t bi = 0; c0.valid; ++bi) {
+    const uint32_t *ids_cur = ids + (bi & 1) * K;
+    uint32_t *ids_nxt = ids + ((bi + 1) & 1) * K;
+    const TileGeom g0 = geom(c0);
+    const Level L = lv[g0.l];
+    uint32_t s0, s1;
+    batch_range(c0, s0, s1);
+    const int ns = static_cast<int>(s1 - s0);
+    const bool last_of_item = c0.k + 1 == item_batches<K>(c0.d);
+    const bool next_new_item = c1.valid && c1.k == 0;
 
-      // owner phase: lane group grp owns positions grp, grp + NGROUPS, ...
-#pragma unroll 1
-      for (int pp = 0; pp < PPG; ++pp) {
-        const int pos_id = grp + pp * NGROUPS;
-        const uint32_t n = pos_id < NPOS ? pcount[pos_id] : 0u;
-        const uint32_t first = pos_id < NPOS ? poff[pos_id] : 0u;
-        const int py = pos_id / TV - 1, px = pos_id % TV - 1;  // tile-local top-left corner
-        const int y0 = y_lo + py, x0 = x_lo + px;              // level coordinates
-        const bool primary = (y0 < 0 ? 0 : y0) >= y_lo && (y0 < 0 ? 0 : y0) < y_lo + T &&
-                             (x0 < 0 ? 0 : x0) >= x_lo && (x0 < 0 ? 0 : x0) < x_lo + T;
-        const bool ok[4] = {y0 >= 0 && x0 >= 0, y0 >= 0 && x0 + 1 < L.w,
-                            y0 + 1 < L.h && x0 >= 0, y0 + 1 < L.h && x0 + 1 < L.w};
-        // the value rows of the four corners (tile-local), when primary
-        float v[4][CPL];
-        if (primary) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            if (ok[c]) {
-              load4ch(vt + ((py + (c >> 1)) * TV + px + (c & 1)) * C + k * CPL, v[c]);
-            } else {
-#pragma unroll
-              for (int jj = 0; jj < CPL; ++jj) v[c][jj] = 0.0f;
-            }
-          }
-        }
-        // the group's positions hold different record counts: loop to the
-        // wave's longest list so the cross-lane sums below see a full wave
-        uint32_t n_wave = n;
-        for (int d = KQ; d < kWave; d <<= 1) n_wave = max(n_wave, __shfl_xor(n_wave, d, kWave));
-        float acc[4][CPL];
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-#pragma unroll
-          for (int jj = 0; jj < CPL; ++jj) acc[d][jj] = 0.0f;
-        constexpr int kUnroll = 4;  // records of one position in flight together
-        for (uint32_t r0i = 0; r0i < n_wave; r0i += kUnroll) {
-          uint4 e[kUnroll];
-          float g[kUnroll][CPL];
-#pragma unroll
-          for (int u = 0; u < kUnroll; ++u) {
-            const uint32_t r = r0i + u;
-            e[u] = stash[r < n ? first + r : 0u];
-            if (r >= n) e[u].w = 0u;  // attention 0: contributes nothing
-            const int q = r < n ? static_cast<int>(e[u].x >> p.lp_log2) : 0;
-            const size_t si = (static_cast<size_t>(b) * s.queries + q) * s.heads + m;
-            load4ch(grad_out + si * C + k * CPL, g[u]);
-          }
-#pragma unroll
-          for (int u = 0; u < kUnroll; ++u) {
-            const bool live = r0i + u < n;
-            const int q = static_cast<int>(e[u].x >> p.lp_log2);
-            const int smp = static_cast<int>(e[u].x & smask);
-            const float wx1 = __uint_as_float(e[u].y), wy1 = __uint_as_float(e[u].z);
-            const float a = __uint_as_float(e[u].w);
-            const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
-            const float cw[4] = {wy0 * wx0, wy0 * wx1, wy1 * wx0, wy1 * wx1};
-#pragma unroll
-            for (int jj = 0; jj < CPL; ++jj) {
-              const float tgv = g[u][jj] * a;
-#pragma unroll
-              for (int d = 0; d < 4; ++d) acc[d][jj] += cw[d] * tgv;
-            }
-            if (primary) {  // uniform per lane group
-              float ga = 0.0f, gx = 0.0f, gy = 0.0f;
-#pragma unroll
-              for (int jj = 0; jj < CPL; ++jj) {
-                const float tgv = g[u][jj] * a;
-                const float val = cw[0] * v[0][jj] + cw[1] * v[1][jj] + cw[2] * v[2][jj] +
-                                  cw[3] * v[3][jj];
-                ga += g[u][jj] * val;
-                gx += tgv * (wy0 * (v[1][jj] - v[0][jj]) + wy1 * (v[3][jj] - v[2][jj]));
-                gy += tgv * (wx0 * (v[2][jj] - v[0][jj]) + wx1 * (v[3][jj] - v[1][jj]));
-              }
-              ga = group_sum<KQ>(ga);
-              gx = group_sum<KQ>(gx);
-              gy = group_sum<KQ>(gy);
-              if (live && k == 0) {
-                const size_t o =
-                    ((static_cast<size_t>(b) * s.queries + q) * s.heads + m) * s.lp + smp;
-                // the reference path's gradient of grid_sample w.r.t. a
-                // sampling location, for tgv = grad_out * attn
-                grad_attn[o] = ga;
-                *reinterpret_cast<float2 *>(grad_loc + 2 * o) =
-                    make_float2(gx * L.fw, gy * L.fh);
-              }
-            }
-          }
-        }
-        // add the position's corner sums to its cells of the four planes;
-        // cell p + d of plane d belongs to position p alone
-        if (n > 0) {
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const int cy = py + (d >> 1), cx = px + (d & 1);
-            if (cy < 0 || cy >= T || cx < 0 || cx >= T) continue;
-            float *dst = planes + (d * T * T + cy * T + cx) * C + k * CPL;
-#pragma unroll
-            for (int jj = 0; jj < CPL; jj += 4) {
-              float4 cur = *reinterpret_cast<float4 *>(dst + jj);
-              cur.x += acc[d][jj];
-              cur.y += acc[d][jj + 1];
-              cur.z += acc[d][jj + 2];
-              cur.w += acc[d][jj + 3];
-              *reinterpret_cast<float4 *>(dst + jj) = cur;
-            }
-          }
-        }
+    // A. sort keys of this batch; its grad_out rows into LDS; the next
+    // batch's ids; prefetch the batch after next and the next value tile;
+    // then the previous batch's gradient stores (after the waits above)
+    int pos = -1;
+    uint32_t rank = 0;
+    uint4 entry = make_uint4(0u, 0u, 0u, 0u);
+    if (tid < ns) {
+      const Tap t = make_tap(__uint_as_float(r_cur.y), __uint_as_float(r_cur.z), L, true);
+      const int py = t.y0 - g0.y_lo + 1, px = t.x0 - g0.x_lo + 1;
+      if (t.in && py >= 0 && py < TV && px >= 0 && px < TV) {  // always, for binned records
+        pos = py * TV + px;
+        entry = make_uint4(static_cast<uint32_t>(tid), __float_as_uint(t.wx1),
+                           __float_as_uint(t.wy1), r_cur.w);
+        rank = atomicAdd(&pcount[pos], 1u);
       }
-      __syncthreads();
     }
-
+#pragma unroll
+    for (int j = 0; j < GROWS; ++j) {
+      *reinterpret_cast<LaneUnit *>(gst + (grp + j * NG) * C + k * CPL) = gregs[j];
+    }
+    if (tid < K) ids_nxt[tid] = r_next.x;
+    const uint4 r_after = load_record(c2);
+    bool v_ok;
+    const uint4 v_next = *value_unit_src(c1, v_ok);
+    if (tid < ns_prev) {
+      grad_attn[f_o] = f_ga;
+      *reinterpret_cast<float2 *>(grad_loc + 2 * static_cast<size_t>(f_o)) =
+          make_float2(f_gx, f_gy);
+    }
     __syncthreads();
 
-    // write-back: cell sum of the four planes, to grad_value or (split tile)
-    // to this chunk's partial tile
-    float *part = split ? partials + (static_cast<size_t>(bm) * p.slot_cap +
-                                      slot_base[static_cast<size_t>(bm) * p.tile_bound + tl] +
-                                      item.y) *
-                                         (T * T * C)
-                        : nullptr;
-    for (int i = threadIdx.x; i < T * T * (C / 4); i += kTileBlock) {
-      const int cell = i / (C / 4), c4 = (i % (C / 4)) * 4;
-      const int yy = cell / T, xx = cell % T;
-      if (y_lo + yy < L.h && x_lo + xx < L.w) {
-        float4 r = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // B. (one wavefront) exclusive scan of the position counts, then the
+    // positions in order of decreasing count (counting sort on min(n, 63))
+    if (tid < kWave) {
+      uint32_t carry = 0;
+      for (int c = 0; c < NPOS; c += kWave) {
+        const int i = c + tid;
+        const uint32_t v = i < NPOS ? pcount[i] : 0u;
+        uint32_t incl = v;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+          const uint32_t up = __shfl_up(incl, d, kWave);
+          if (tid >= d) incl += up;
+        }
+        if (i < NPOS) poff[i] = carry + incl - v;
+        carry += __shfl(incl, kWave - 1, kWave);
+      }
+      bucket[tid] = 0;
+      for (int i = tid; i < NPOS; i += kWave) atomicAdd(&bucket[63 - min(pcount[i], 63u)], 1u);
+      const uint32_t v = bucket[tid];
+      uint32_t incl = v;
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t up = __shfl_up(incl, d, kWave);
+        if (tid >= d) incl += up;
+      }
+      bucket[tid] = incl - v;
+      for (int i = tid; i < NPOS; i += kWave) {
+        order[atomicAdd(&bucket[63 - min(pcount[i], 63u)], 1u)] = static_cast<uint32_t>(i);
+      }
+    }
+    __syncthreads();
+
+    // C. records in position order
+    if (pos >= 0) stash[poff[pos] + rank] = entry;
+    __syncthreads();
+
+    // D. next batch's grad_out rows in flight; write back the item the
+    // previous batch finished; then reduce this batch
+#pragma unroll
+    for (int j = 0; j < GROWS; ++j) gregs[j] = *grow_src(c1, ids_nxt, j);
+    if (wb_pending) {
+      write_back(wb_item);
+      __syncthreads();
+    }
+#pragma unroll 1
+    for (int i = grp; i < NPOS; i += NG) {
+      const int p_id = static_cast<int>(order[i]);
+      const uint32_t n = pcount[p_id];
+      if (n == 0) break;  // positions are in order of decreasing count
+      const uint32_t first = poff[p_id];
+      const int py = p_id / TV - 1, px = p_id % TV - 1;  // tile frame, >= -1
+      // corner value rows (row -1 or column -1: the zero row after the tile)
+      const VT *vrow[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int cy = py + (d >> 1), cx = px + (d & 1);
+        vrow[d] = vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * C : NPOS * C) + k * CPL;
+      }
+      float v[4][CPL];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) load4ch(vrow[d], v[d]);
+      float acc[4][CPL];
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) acc[d][j] = 0.0f;
+      uint4 e = stash[first];
+      for (uint32_t r = 0; r < n; ++r) {
+        const uint4 e_next = stash[first + min(r + 1, n - 1)];
+        const int t = static_cast<int>(e.x);
+        const float wx1 = __uint_as_float(e.y), wy1 = __uint_as_float(e.z);
+        const float a = __uint_as_float(e.w);
+        const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
+        const float wa[4] = {wy0 * wx0 * a, wy0 * wx1 * a, wy1 * wx0 * a, wy1 * wx1 * a};
+        float gv[CPL];
+        load4ch(gst + t * C + k * CPL, gv);
+        float D[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          const float4 v = *reinterpret_cast<const float4 *>(planes + (d * T * T + cell) * C + c4);
-          r.x += v.x;
-          r.y += v.y;
-          r.z += v.z;
-          r.w += v.w;
+          float dd = 0.0f;
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            acc[d][j] += wa[d] * gv[j];
+            dd += gv[j] * v[d][j];
+          }
+          D[d] = group_sum<KQ>(dd);
         }
-        float *dst = split ? part + cell * C + c4
-                           : grad_value + slab +
-                                 static_cast<size_t>(L.start + (y_lo + yy) * L.w + x_lo + xx) * MC +
-                                 c4;
-        *reinterpret_cast<float4 *>(dst) = r;
+        // D_0..D_3 replace the start of grad_out row t (read by this group
+        // alone, above); the gradients are finished per record in E
+        if (k == 0) *reinterpret_cast<float4 *>(gst + t * C) = make_float4(D[0], D[1], D[2], D[3]);
+        e = e_next;
+      }
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        float4 *dst = reinterpret_cast<float4 *>(planes + (d * NPOS + p_id) * C + k * CPL);
+        float4 cur = *dst;
+        cur.x += acc[d][0];
+        cur.y += acc[d][1];
+        cur.z += acc[d][2];
+        cur.w += acc[d][3];
+        *dst = cur;
       }
     }
     __syncthreads();
-  }
-}
 
-// ---------------------------------------------------------- 5. combine ---
-
-// Sum the partial tiles of every split tile in chunk order (deterministic for
-// a given split) and store the cells' gradients.
-template <int C, int T>
-__global__ void __launch_bounds__(kBinBlock)
-    msda_tile_combine(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
-                      Shape s, BinPlan p, const uint32_t *__restrict__ tile_start,
-                      const SlabMeta *__restrict__ meta, const uint32_t *__restrict__ slot_base,
-                      const uint32_t *__restrict__ multi, const float *__restrict__ partials,
-                      float *__restrict__ grad_value) {
-  __shared__ Level lv[kMaxLevels];
-  __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
-  stage_levels(lv, shapes, starts, s);
-  stage_tiles<T>(lv, s.levels, ntc, base);
-  const int bm = blockIdx.x / kCombineBlocksPerSlab, r = blockIdx.x % kCombineBlocksPerSlab;
-  const SlabMeta mt = meta[bm];
-  const int b = bm / s.heads, m = bm % s.heads;
-  const int MC = s.heads * C;
-  const size_t slab = static_cast<size_t>(b) * s.spatial * MC + m * C;
-  const uint32_t *ts = tile_start + static_cast<size_t>(bm) * (p.tile_bound + 1);
-  for (uint32_t i = 0; i < mt.nmulti; ++i) {
-    const int tl = static_cast<int>(multi[static_cast<size_t>(bm) * p.tile_bound + i]);
-    const uint32_t n = ts[tl + 1] - ts[tl];
-    const uint32_t chunks = (n + mt.rmax - 1) / mt.rmax;
-    const float *part0 = partials + (static_cast<size_t>(bm) * p.slot_cap +
-                                     slot_base[static_cast<size_t>(bm) * p.tile_bound + tl]) *
-                                        (T * T * C);
-    const TileGeom tg = tile_geom(tl, T, ntc, base);
-    const Level L = lv[tg.l];
-    // the slab's blocks split each tile's cells between them
-    for (int e = r * blockDim.x + threadIdx.x; e < T * T * (C / 4);
-         e += kCombineBlocksPerSlab * blockDim.x) {
-      const int cell = e / (C / 4), c4 = (e % (C / 4)) * 4;
-      const int yy = cell / T, xx = cell % T;
-      if (tg.y_lo + yy >= L.h || tg.x_lo + xx >= L.w) continue;
-      float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      for (uint32_t k = 0; k < chunks; ++k) {
-        const float4 v =
-            *reinterpret_cast<const float4 *>(part0 + static_cast<size_t>(k) * (T * T * C) +
-                                              cell * C + c4);
-        acc.x += v.x;
-        acc.y += v.y;
-        acc.z += v.z;
-        acc.w += v.w;
-      }
-      float *dst = grad_value + slab +
-                   static_cast<size_t>(L.start + (tg.y_lo + yy) * L.w + tg.x_lo + xx) * MC + c4;
-      *reinterpret_cast<float4 *>(dst) = acc;
+    // E. this batch's location/weight gradients (stored in the next A),
+    // position counts reset, next value tile staged
+    if (tid < ns) finish_record(tid, ids_cur, c0.d, L, f_o, f_ga, f_gx, f_gy);
+    if (tid < NPOS) pcount[tid] = 0;
+    if (next_new_item && tid < NPOS * UPV) {
+      reinterpret_cast<uint4 *>(vt)[tid] = v_ok ? v_next : make_uint4(0u, 0u, 0u, 0u);
     }
+    ns_prev = ns;
+    wb_pending = last_of_item;
+    wb_item = c0.d;
+    r_cur = r_next;
+    r_next = r_after;
+    c0 = c1;
+    c1 = c2;
+    c2 = advance(c2);
+    __syncthreads();
   }
+  if (tid < ns_prev) {
+    grad_attn[f_o] = f_ga;
+    *reinterpret_cast<float2 *>(grad_loc + 2 * static_cast<size_t>(f_o)) = make_float2(f_gx, f_gy);
+  }
+  if (wb_pending) write_back(wb_item);
 }
 
 }  // namespace msda

@@ -12,6 +12,7 @@
 #include <climits>
 #include <cstdint>
 #include <initializer_list>
+#include <type_traits>
 #include <cstdarg>
 #include <cstdio>
 
@@ -286,59 +287,37 @@ void launch_backward_atomic(const void *value, const int64_t *shapes, const int6
   }
 }
 
-// Tile edge of the tile-owned backward per channel count (about 150 KB of
-// LDS per workgroup, one 1024-thread workgroup per CU).
-int tile_edge(int channels) {
-  return channels == 16 ? msda::TileEdge<16>::value
-                        : (channels == 32 ? msda::TileEdge<32>::value : msda::TileEdge<64>::value);
-}
-
 size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
-// Scratch layout of the tile-owned backward.
-struct TileWorkspace {
-  msda::BinPlan plan;
-  size_t counts, tile_start, records, meta, items, slot_base, multi, partials, bytes;
-};
+// Tile edge and batch size of the tile-owned backward per value dtype and
+// channel count (0 when the tile path does not cover the channel count).
+template <typename VT>
+int tile_edge_for(int channels) {
+  switch (channels) {
+    case 16: return msda::TileCfg<VT, 16>::T;
+    case 32: return msda::TileCfg<VT, 32>::T;
+    case 64: return msda::TileCfg<VT, 64>::T;
+    default: return 0;
+  }
+}
 
-constexpr size_t kPartialPoolBytes = size_t{256} << 20;  // split-tile partials, all slabs
+template <typename VT>
+int tile_batch_for(int channels) {
+  switch (channels) {
+    case 16: return msda::TileCfg<VT, 16>::K;
+    case 32: return msda::TileCfg<VT, 32>::K;
+    default: return msda::TileCfg<VT, 64>::K;
+  }
+}
 
-bool plan_tile_workspace(const msda::Shape &s, TileWorkspace &w) {
-  if (s.channels != 16 && s.channels != 32 && s.channels != 64) return false;
-  const int T = tile_edge(s.channels);
-  msda::BinPlan &p = w.plan;
-  p.chunk_q = msda::kBinBlock;
-  p.chunks = (s.queries + p.chunk_q - 1) / p.chunk_q;
-  // tiles of one level < 3*H*W/T + 1, so 3*spatial/T + levels + 1 bounds a slab
-  const int64_t bound = 3 * static_cast<int64_t>(s.spatial) / T + s.levels + 1;
-  if (bound > msda::kMaxTilesPerSlab) return false;
-  p.tile_bound = static_cast<int>(bound);
-  p.lp_log2 = log2_int(s.lp > 0 ? s.lp : 1);
-  if ((static_cast<int64_t>(s.queries) << p.lp_log2) > (int64_t{1} << 32)) return false;
-  p.rec_cap = 4 * static_cast<int64_t>(s.queries) * s.lp;
-  if (p.rec_cap >= (int64_t{1} << 31)) return false;
-  const int64_t bm = static_cast<int64_t>(s.batch) * s.heads;
-  const size_t tile_floats = static_cast<size_t>(T) * T * s.channels;
-  p.rmax0 = 2048;
-  int64_t slots = static_cast<int64_t>(kPartialPoolBytes / (bm * tile_floats * 4));
-  p.slot_cap = static_cast<int>(slots < 32 ? 32 : (slots > (1 << 20) ? (1 << 20) : slots));
-  p.item_cap = p.tile_bound + p.slot_cap;
-  size_t off = 0;
-  auto take = [&off](size_t bytes) {
-    const size_t at = off;
-    off = align256(off + bytes);
-    return at;
-  };
-  w.counts = take(static_cast<size_t>(bm) * p.chunks * p.tile_bound * 4);
-  w.tile_start = take(static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
-  w.records = take(static_cast<size_t>(bm) * p.rec_cap * 4);
-  w.meta = take(static_cast<size_t>(bm) * sizeof(msda::SlabMeta));
-  w.items = take(static_cast<size_t>(bm) * p.item_cap * sizeof(uint2));
-  w.slot_base = take(static_cast<size_t>(bm) * p.tile_bound * 4);
-  w.multi = take(static_cast<size_t>(bm) * p.tile_bound * 4);
-  w.partials = take(static_cast<size_t>(bm) * p.slot_cap * tile_floats * 4);
-  w.bytes = off;
-  return true;
+int tile_batch(int value_dtype, int channels) {
+  return value_dtype == MUSPACE_DTYPE_F32 ? tile_batch_for<float>(channels)
+                                          : tile_batch_for<msda::bf16_t>(channels);
+}
+
+int tile_edge(int value_dtype, int channels) {
+  return value_dtype == MUSPACE_DTYPE_F32 ? tile_edge_for<float>(channels)
+                                          : tile_edge_for<msda::bf16_t>(channels);  // fp16: same
 }
 
 // Persistent grid of the tile kernel: one workgroup per CU, a multiple of 8
@@ -346,7 +325,7 @@ bool plan_tile_workspace(const msda::Shape &s, TileWorkspace &w) {
 int tile_grid() {
   static int cached[64] = {0};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
   if (cached[dev] == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -358,21 +337,64 @@ int tile_grid() {
   return cached[dev];
 }
 
+// Scratch layout of the tile-owned backward.
+struct TileWorkspace {
+  msda::BinPlan plan;
+  size_t counts, tile_start, records, items, item_total, bytes;
+};
+
+bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w) {
+  const int T = tile_edge(value_dtype, s.channels);
+  if (T == 0) return false;
+  msda::BinPlan &p = w.plan;
+  p.chunk_q = msda::kBinBlock;
+  p.chunks = (s.queries + p.chunk_q - 1) / p.chunk_q;
+  // a level of n cells has ceil(h/T)*ceil(w/T) <= n/T + 1 tiles
+  const int64_t bound = static_cast<int64_t>(s.spatial) / T + s.levels + 1;
+  if (bound > msda::kMaxTilesPerSlab) return false;
+  p.tile_bound = static_cast<int>(bound);
+  p.lp_log2 = log2_int(s.lp > 0 ? s.lp : 1);
+  if ((static_cast<int64_t>(s.queries) << p.lp_log2) > (int64_t{1} << 32)) return false;
+  p.rec_cap = static_cast<int64_t>(s.queries) * s.lp;
+  if (p.rec_cap >= (int64_t{1} << 31)) return false;
+  const int64_t bm = static_cast<int64_t>(s.batch) * s.heads;
+  // records per work item: about 16 items per workgroup, in whole batches
+  const int K = tile_batch(value_dtype, s.channels);
+  const int64_t total = bm * p.rec_cap;
+  if (total >= (int64_t{1} << 32)) return false;  // sample indices are 32-bit in the tile kernel
+  int64_t mult = (total + int64_t{16} * tile_grid() * K - 1) / (int64_t{16} * tile_grid() * K);
+  mult = mult < 1 ? 1 : (mult > 64 ? 64 : mult);
+  p.rmax = static_cast<int>(mult * K);
+  const int64_t item_cap = bm * (p.tile_bound + (p.rec_cap + p.rmax - 1) / p.rmax + 1);
+  if (item_cap >= (int64_t{1} << 31)) return false;
+  p.item_cap = static_cast<int>(item_cap);
+  size_t off = 0;
+  auto take = [&off](size_t bytes) {
+    const size_t at = off;
+    off = align256(off + bytes);
+    return at;
+  };
+  w.counts = take(static_cast<size_t>(bm) * p.chunks * p.tile_bound * 4);
+  w.tile_start = take(static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
+  w.records = take(static_cast<size_t>(bm) * p.rec_cap * 16);
+  w.items = take(static_cast<size_t>(p.item_cap) * sizeof(msda::Item));
+  w.item_total = take(4);
+  w.bytes = off;
+  return true;
+}
+
 template <typename VT, typename GT, int C>
 void launch_backward_tiles(const void *value, const int64_t *shapes, const int64_t *starts,
                            const void *loc, const void *attn, const void *grad_out, float *gv,
                            float *gl, float *ga, const msda::Shape &s, const TileWorkspace &w,
                            void *workspace, hipStream_t st) {
-  constexpr int T = msda::TileEdge<C>::value;
+  constexpr int T = msda::TileCfg<VT, C>::T;
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + w.counts);
   uint32_t *tile_start = reinterpret_cast<uint32_t *>(ws + w.tile_start);
-  uint32_t *records = reinterpret_cast<uint32_t *>(ws + w.records);
-  msda::SlabMeta *meta = reinterpret_cast<msda::SlabMeta *>(ws + w.meta);
-  uint2 *items = reinterpret_cast<uint2 *>(ws + w.items);
-  uint32_t *slot_base = reinterpret_cast<uint32_t *>(ws + w.slot_base);
-  uint32_t *multi = reinterpret_cast<uint32_t *>(ws + w.multi);
-  float *partials = reinterpret_cast<float *>(ws + w.partials);
+  uint4 *records = reinterpret_cast<uint4 *>(ws + w.records);
+  msda::Item *items = reinterpret_cast<msda::Item *>(ws + w.items);
+  uint32_t *item_total = reinterpret_cast<uint32_t *>(ws + w.item_total);
   const msda::BinPlan &p = w.plan;
   const int bm = s.batch * s.heads;
   const VT *v = static_cast<const VT *>(value);
@@ -381,10 +403,10 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   const VT *go = static_cast<const VT *>(grad_out);
   const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4;
 
-  auto count = msda::msda_bin_count<GT, T>;
+  auto count = msda::msda_bin_count<GT, C, T>;
   auto scatter = msda::msda_bin_scatter<GT, T>;
-  auto tile = msda::msda_tile_backward<VT, GT, C, T>;
-  const size_t tile_bytes = msda::tile_lds_bytes<T>(C, sizeof(VT));
+  auto tile = msda::msda_tile_backward<VT, C>;
+  constexpr size_t tile_bytes = msda::tile_lds_bytes<VT, C>();
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(count),
                             hipFuncAttributeMaxDynamicSharedMemorySize, hist_bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(scatter),
@@ -392,17 +414,14 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(tile),
                             hipFuncAttributeMaxDynamicSharedMemorySize, tile_bytes);
 
-  count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts, gl,
-                                                             ga);
-  msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
-      shapes, starts, s, p, counts, tile_start, meta, items, slot_base, multi, gv);
-  scatter<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts,
-                                                               records);
-  tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, shapes, starts, lc, aw, go, records,
-                                                          tile_start, meta, items, slot_base, s,
-                                                          p, gv, partials, gl, ga);
-  msda::msda_tile_combine<C, T><<<bm * msda::kCombineBlocksPerSlab, msda::kBinBlock, 0, st>>>(
-      shapes, starts, s, p, tile_start, meta, slot_base, multi, partials, gv);
+  count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts,
+                                                             item_total, gv, gl, ga);
+  msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(shapes, starts, s, p, counts,
+                                                            tile_start, item_total, items, gv);
+  scatter<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, aw, s, p,
+                                                               counts, records);
+  tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, shapes, starts, go, records, items,
+                                                          item_total, s, p, gv, gl, ga);
 }
 
 template <typename VT, typename GT>
@@ -410,8 +429,10 @@ void launch_backward(const void *value, const int64_t *shapes, const int64_t *st
                      const void *loc, const void *attn, const void *grad_out, float *gv,
                      float *gl, float *ga, const msda::Shape &s, void *workspace,
                      size_t workspace_bytes, hipStream_t st) {
+  constexpr int value_dtype = std::is_same<VT, float>::value ? MUSPACE_DTYPE_F32
+                                                             : MUSPACE_DTYPE_F16;
   TileWorkspace w;
-  const bool tiles = plan_tile_workspace(s, w) && workspace != nullptr &&
+  const bool tiles = plan_tile_workspace(s, value_dtype, w) && workspace != nullptr &&
                      workspace_bytes >= w.bytes && rows_aligned({value, grad_out, gv}, gl) &&
                      aligned(workspace, 256);
   if (!tiles) {
@@ -558,7 +579,7 @@ size_t ms_deform_attn_backward_workspace_size(int value_dtype, int64_t batch,
   }
   ok();
   TileWorkspace w;
-  if (!needs_data(s) || s.lp == 0 || !plan_tile_workspace(s, w)) return 0;
+  if (!needs_data(s) || s.lp == 0 || !plan_tile_workspace(s, value_dtype, w)) return 0;
   return w.bytes;
 }
 
@@ -602,7 +623,7 @@ int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *s
   // stream-ordered scratch of the tile-owned path; freed in stream order
   size_t bytes = 0;
   TileWorkspace w;
-  if (needs_data(s) && s.lp > 0 && plan_tile_workspace(s, w)) bytes = w.bytes;
+  if (needs_data(s) && s.lp > 0 && plan_tile_workspace(s, value_dtype, w)) bytes = w.bytes;
   void *workspace = nullptr;
   if (bytes > 0 && hipMallocAsync(&workspace, bytes, st) != hipSuccess) {
     (void)hipGetLastError();
