@@ -14,9 +14,12 @@ synthetic inputs resident in HBM before timing.
 
 value = effective GB/s = algorithmic bytes of fwd+bwd / measured time per step
 (byte model: every tensor once at its storage width; see muspace_amd/workloads.py).
-The roofline entry prices the dominant kernel (the backward) against the
-8 TB/s HBM peak, from HIP events around each of its launches in the timed
-region. cpu_baseline times the oracle (a CPU restatement of the reference's
+The roofline entry prices the dominant launch -- the backward entry point,
+one C-ABI call that runs four kernels (bin_count, bin_scan, bin_scatter,
+tile_backward) -- against the 8 TB/s HBM peak, from HIP events around each
+backward call in the timed region; `traffic` is the measured HBM bytes of
+those four kernels per call (rocprofv3 FETCH_SIZE/WRITE_SIZE, calibrated on a
+copy kernel) when profiles/traffic_c2_fp32.json holds them. cpu_baseline times the oracle (a CPU restatement of the reference's
 PyTorch path) on a query subset of the same workload.
 """
 
@@ -262,7 +265,8 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "msda_backward_rows<float,float,32,4>",
+            "kernel": "ms_deform_attn_backward (msda_bin_count, msda_bin_scan, "
+                      "msda_bin_scatter, msda_tile_backward<float,32>)",
             "achieved": round(bwd_achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

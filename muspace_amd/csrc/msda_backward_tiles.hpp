@@ -74,6 +74,7 @@ struct Item {
   uint32_t r1, y_lo, x_lo, pad;
 };
 constexpr uint32_t kSplitBit = 0x80000000u;
+constexpr uint32_t kNoRecord = 0xffffffffu;  // sample with no corner inside its level
 constexpr uint32_t kTileIndexMask = 0xffffu;
 
 // Tile-kernel configuration per (value type, channels): tile edge T, batch
@@ -201,8 +202,7 @@ __global__ void __launch_bounds__(kBinBlock)
     msda_bin_count(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                    const GT *__restrict__ loc, Shape s, BinPlan p,
                    uint32_t *__restrict__ counts, uint32_t *__restrict__ item_total,
-                   float *__restrict__ grad_value, float *__restrict__ grad_loc,
-                   float *__restrict__ grad_attn) {
+                   float *__restrict__ grad_value) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
   extern __shared__ uint32_t hist[];
@@ -226,12 +226,7 @@ __global__ void __launch_bounds__(kBinBlock)
     const size_t o = (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp;
     const int l = level_of_sample(smp, s);
     const Tap t = make_tap(to_float(loc[2 * o]), to_float(loc[2 * o + 1]), lv[l], true);
-    if (!t.in) {
-      grad_attn[o] = 0.0f;
-      *reinterpret_cast<float2 *>(grad_loc + 2 * o) = make_float2(0.0f, 0.0f);
-      continue;
-    }
-    atomicAdd(&hist[primary_tile<T>(t, ntc[l], base[l])], 1u);
+    if (t.in) atomicAdd(&hist[primary_tile<T>(t, ntc[l], base[l])], 1u);
   }
 
   // boundary cells of the slab's tiles ch, ch + chunks, ...
@@ -373,7 +368,8 @@ template <typename GT, int T>
 __global__ void __launch_bounds__(kBinBlock)
     msda_bin_scatter(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                      const GT *__restrict__ loc, const GT *__restrict__ attn, Shape s, BinPlan p,
-                     const uint32_t *__restrict__ counts, uint4 *__restrict__ records) {
+                     const uint32_t *__restrict__ counts, uint4 *__restrict__ records,
+                     uint32_t *__restrict__ rec_of_sample) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
   extern __shared__ uint32_t cursor[];
@@ -397,11 +393,15 @@ __global__ void __launch_bounds__(kBinBlock)
     const int l = level_of_sample(smp, s);
     const float lx = to_float(loc[2 * o]), ly = to_float(loc[2 * o + 1]);
     const Tap t = make_tap(lx, ly, lv[l], true);
-    if (!t.in) continue;
+    if (!t.in) {
+      rec_of_sample[o] = kNoRecord;
+      continue;
+    }
     const uint32_t id = (static_cast<uint32_t>(q) << p.lp_log2) | static_cast<uint32_t>(smp);
     const uint32_t at = atomicAdd(&cursor[primary_tile<T>(t, ntc[l], base[l])], 1u);
     rec[at] = make_uint4(id, __float_as_uint(lx), __float_as_uint(ly),
                          __float_as_uint(to_float(attn[o])));
+    rec_of_sample[o] = at;
   }
 }
 
@@ -440,10 +440,9 @@ template <typename VT, int C>
 __global__ void __launch_bounds__(kTileBlock)
     msda_tile_backward(const VT *__restrict__ value, const int64_t *__restrict__ shapes,
                        const int64_t *__restrict__ starts, const VT *__restrict__ grad_out,
-                       const uint4 *__restrict__ records, const Item *__restrict__ items,
+                       uint4 *__restrict__ records, const Item *__restrict__ items,
                        const uint32_t *__restrict__ item_total, Shape s, BinPlan p,
-                       float *__restrict__ grad_value, float *__restrict__ grad_loc,
-                       float *__restrict__ grad_attn) {
+                       float *__restrict__ grad_value) {
   using Cfg = TileCfg<VT, C>;
   constexpr int T = Cfg::T, K = Cfg::K, CPL = Cfg::CPL;
   constexpr int TV = T + 1, NPOS = TV * TV;
@@ -570,22 +569,16 @@ __global__ void __launch_bounds__(kTileBlock)
         grad_out + ((static_cast<size_t>(b) * s.queries + q) * s.heads + m) * C + k * CPL);
   };
   const uint32_t smask = (1u << p.lp_log2) - 1u;
-  // location and weight gradients of sorted record j of a finished batch:
-  // stash[j] = {t, wx1, wy1, attn}, the owner left D_0..D_3 at the start of
-  // grad_out row t, bid = the batch's record ids
-  auto finish_record = [&](int j, const uint32_t *bid, const Item &d, const Level &Lf,
-                           uint32_t &o, float &ga, float &gx, float &gy) {
-    const uint4 e = stash[j];
-    const int t = static_cast<int>(e.x);
+  // location and weight gradients of record t (batch order) of a finished
+  // batch, from its sorted slot (stash[slot] = {t, wx1, wy1, attn}) and the
+  // D_0..D_3 the owner left at the start of grad_out row t
+  auto finish_record = [&](int t, uint32_t slot, const Level &Lf, float &ga, float &gx,
+                           float &gy) {
+    const uint4 e = stash[slot];
     const float4 D = *reinterpret_cast<const float4 *>(gst + t * C);
     const float wx1 = __uint_as_float(e.y), wy1 = __uint_as_float(e.z);
     const float a = __uint_as_float(e.w);
     const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
-    const uint32_t id = bid[t];
-    const int b = static_cast<int>(d.b), m = static_cast<int>(d.m);
-    const int q = static_cast<int>(id >> p.lp_log2), smp = static_cast<int>(id & smask);
-    o = static_cast<uint32_t>(((static_cast<size_t>(b) * s.queries + q) * s.heads + m) * s.lp +
-                              smp);
     ga = wy0 * (wx0 * D.x + wx1 * D.y) + wy1 * (wx0 * D.z + wx1 * D.w);
     gx = a * (wy0 * (D.y - D.x) + wy1 * (D.w - D.z)) * Lf.fw;
     gy = a * (wx0 * (D.z - D.x) + wx1 * (D.w - D.y)) * Lf.fh;
@@ -643,8 +636,10 @@ __global__ void __launch_bounds__(kTileBlock)
 #pragma unroll
   for (int j = 0; j < GROWS; ++j) gregs[j] = *grow_src(c0, ids, j);
 
-  int ns_prev = 0;        // records of the previous batch (gradients pending)
-  uint32_t f_o = 0;       // this thread's pending location/weight gradients
+  // the previous batch's location/weight gradients of this thread's record,
+  // stored over that (consumed) record during the next batch
+  int ns_prev = 0;
+  size_t f_at = 0;
   float f_ga = 0.0f, f_gx = 0.0f, f_gy = 0.0f;
   bool wb_pending = false;  // the previous batch finished an item
   Item wb_item{0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
@@ -684,9 +679,8 @@ __global__ void __launch_bounds__(kTileBlock)
     bool v_ok;
     const uint4 v_next = *value_unit_src(c1, v_ok);
     if (tid < ns_prev) {
-      grad_attn[f_o] = f_ga;
-      *reinterpret_cast<float2 *>(grad_loc + 2 * static_cast<size_t>(f_o)) =
-          make_float2(f_gx, f_gy);
+      records[f_at] = make_uint4(__float_as_uint(f_ga), __float_as_uint(f_gx),
+                                 __float_as_uint(f_gy), 0u);
     }
     __syncthreads();
 
@@ -723,7 +717,11 @@ __global__ void __launch_bounds__(kTileBlock)
     __syncthreads();
 
     // C. records in position order
-    if (pos >= 0) stash[poff[pos] + rank] = entry;
+    uint32_t my_slot = 0;
+    if (pos >= 0) {
+      my_slot = poff[pos] + rank;
+      stash[my_slot] = entry;
+    }
     __syncthreads();
 
     // D. next batch's grad_out rows in flight; write back the item the
@@ -797,7 +795,10 @@ __global__ void __launch_bounds__(kTileBlock)
 
     // E. this batch's location/weight gradients (stored in the next A),
     // position counts reset, next value tile staged
-    if (tid < ns) finish_record(tid, ids_cur, c0.d, L, f_o, f_ga, f_gx, f_gy);
+    if (tid < ns) {
+      finish_record(tid, my_slot, L, f_ga, f_gx, f_gy);
+      f_at = static_cast<size_t>(c0.d.b * s.heads + c0.d.m) * p.rec_cap + s0 + tid;
+    }
     if (tid < NPOS) pcount[tid] = 0;
     if (next_new_item && tid < NPOS * UPV) {
       reinterpret_cast<uint4 *>(vt)[tid] = v_ok ? v_next : make_uint4(0u, 0u, 0u, 0u);
@@ -813,10 +814,40 @@ __global__ void __launch_bounds__(kTileBlock)
     __syncthreads();
   }
   if (tid < ns_prev) {
-    grad_attn[f_o] = f_ga;
-    *reinterpret_cast<float2 *>(grad_loc + 2 * static_cast<size_t>(f_o)) = make_float2(f_gx, f_gy);
+    records[f_at] = make_uint4(__float_as_uint(f_ga), __float_as_uint(f_gx),
+                               __float_as_uint(f_gy), 0u);
   }
   if (wb_pending) write_back(wb_item);
+}
+
+// -------------------------------------------------------------- 5. gather ---
+
+// Location and attention-weight gradients in sample order: sample o's
+// record slot holds {grad_attn, grad_loc_x, grad_loc_y} after the tile
+// kernel. Blocks walk the samples slab by slab (XCD-contiguous), so the
+// record reads of one block stay inside one slab's record range and the
+// stores are whole lines.
+__global__ void __launch_bounds__(kBinBlock)
+    msda_grad_gather(const uint32_t *__restrict__ rec_of_sample, const uint4 *__restrict__ records,
+                     Shape s, BinPlan p, int blocks_per_slab, float *__restrict__ grad_loc,
+                     float *__restrict__ grad_attn) {
+  const int lb = xcd_logical_block(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int bm = lb / blocks_per_slab;
+  const int j = (lb % blocks_per_slab) * kBinBlock + static_cast<int>(threadIdx.x);
+  if (j >= s.queries * s.lp) return;
+  const int q = j / s.lp, smp = j % s.lp;
+  const int b = bm / s.heads, m = bm % s.heads;
+  const size_t o = ((static_cast<size_t>(b) * s.queries + q) * s.heads + m) * s.lp + smp;
+  const uint32_t r = rec_of_sample[o];
+  float ga = 0.0f, gx = 0.0f, gy = 0.0f;
+  if (r != kNoRecord) {
+    const uint4 v = records[static_cast<size_t>(bm) * p.rec_cap + r];
+    ga = __uint_as_float(v.x);
+    gx = __uint_as_float(v.y);
+    gy = __uint_as_float(v.z);
+  }
+  grad_attn[o] = ga;
+  *reinterpret_cast<float2 *>(grad_loc + 2 * o) = make_float2(gx, gy);
 }
 
 }  // namespace msda

@@ -340,7 +340,7 @@ int tile_grid() {
 // Scratch layout of the tile-owned backward.
 struct TileWorkspace {
   msda::BinPlan plan;
-  size_t counts, tile_start, records, items, item_total, bytes;
+  size_t counts, tile_start, records, rec_of_sample, items, item_total, bytes;
 };
 
 bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w) {
@@ -377,6 +377,7 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   w.counts = take(static_cast<size_t>(bm) * p.chunks * p.tile_bound * 4);
   w.tile_start = take(static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
   w.records = take(static_cast<size_t>(bm) * p.rec_cap * 16);
+  w.rec_of_sample = take(static_cast<size_t>(bm) * p.rec_cap * 4);
   w.items = take(static_cast<size_t>(p.item_cap) * sizeof(msda::Item));
   w.item_total = take(4);
   w.bytes = off;
@@ -393,6 +394,7 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + w.counts);
   uint32_t *tile_start = reinterpret_cast<uint32_t *>(ws + w.tile_start);
   uint4 *records = reinterpret_cast<uint4 *>(ws + w.records);
+  uint32_t *rec_of_sample = reinterpret_cast<uint32_t *>(ws + w.rec_of_sample);
   msda::Item *items = reinterpret_cast<msda::Item *>(ws + w.items);
   uint32_t *item_total = reinterpret_cast<uint32_t *>(ws + w.item_total);
   const msda::BinPlan &p = w.plan;
@@ -415,13 +417,16 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
                             hipFuncAttributeMaxDynamicSharedMemorySize, tile_bytes);
 
   count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts,
-                                                             item_total, gv, gl, ga);
+                                                             item_total, gv);
   msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(shapes, starts, s, p, counts,
                                                             tile_start, item_total, items, gv);
   scatter<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, aw, s, p,
-                                                               counts, records);
+                                                               counts, records, rec_of_sample);
   tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, shapes, starts, go, records, items,
-                                                          item_total, s, p, gv, gl, ga);
+                                                          item_total, s, p, gv);
+  const int per_slab = static_cast<int>((p.rec_cap + msda::kBinBlock - 1) / msda::kBinBlock);
+  msda::msda_grad_gather<<<bm * per_slab, msda::kBinBlock, 0, st>>>(rec_of_sample, records, s, p,
+                                                                    per_slab, gl, ga);
 }
 
 template <typename VT, typename GT>
