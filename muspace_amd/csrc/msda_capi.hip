@@ -142,8 +142,9 @@ Launch plan_rows(const msda::Shape &s, int kq) {
   const int need = (s.lp + gu - 1) / gu;
   Launch L;
   L.ns = need <= 1 ? 1 : (need <= 2 ? 2 : 4);
+  if (L.ns > kq) L.ns = kq;  // the forward computes one tap per lane: ng * ns <= 64
   L.plan.gu_log2 = log2_int(gu);
-  L.plan.iters = 2;
+  L.plan.iters = 8;  // units per lane group: the next unit's geometry loads overlap the gathers
   const int64_t units_per_wave_iter = ng / gu;
   const int64_t wave_iters = (s.units + units_per_wave_iter - 1) / units_per_wave_iter;
   const int64_t waves = (wave_iters + L.plan.iters - 1) / L.plan.iters;
@@ -160,6 +161,10 @@ int generic_blocks(int64_t work) {
 }
 
 bool needs_data(const msda::Shape &s) { return s.units > 0; }
+
+size_t value_bytes(const msda::Shape &s, size_t elem) {
+  return static_cast<size_t>(s.batch) * s.spatial * s.heads * s.channels * elem;
+}
 
 bool aligned(const void *p, uintptr_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
@@ -188,18 +193,23 @@ void launch_forward_rows(const void *value, const int64_t *shapes, const int64_t
   const GT *lc = static_cast<const GT *>(loc);
   const GT *aw = static_cast<const GT *>(attn);
   VT *o = static_cast<VT *>(out);
+  const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
   switch (L.ns) {
     case 1:
       msda::msda_forward_rows<VT, GT, C, 1>
-          <<<L.blocks, msda::kBlock, 0, st>>>(v, shapes, starts, lc, aw, o, s, L.plan);
+          <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, o, s, L.plan);
       break;
     case 2:
-      msda::msda_forward_rows<VT, GT, C, 2>
-          <<<L.blocks, msda::kBlock, 0, st>>>(v, shapes, starts, lc, aw, o, s, L.plan);
+      if constexpr (KQ >= 2) {
+        msda::msda_forward_rows<VT, GT, C, 2>
+            <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, o, s, L.plan);
+      }
       break;
     default:
-      msda::msda_forward_rows<VT, GT, C, 4>
-          <<<L.blocks, msda::kBlock, 0, st>>>(v, shapes, starts, lc, aw, o, s, L.plan);
+      if constexpr (KQ >= 4) {
+        msda::msda_forward_rows<VT, GT, C, 4>
+            <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, o, s, L.plan);
+      }
       break;
   }
 }
@@ -208,7 +218,9 @@ template <typename VT, typename GT>
 void launch_forward(const void *value, const int64_t *shapes, const int64_t *starts,
                     const void *loc, const void *attn, void *out, const msda::Shape &s,
                     hipStream_t st) {
-  const int rows = rows_aligned({value, out}) ? s.channels : 0;
+  // the row kernel addresses value with 32-bit byte offsets below kOobOffset
+  const bool small = value_bytes(s, sizeof(VT)) + 64 <= msda::kOobOffset;
+  const int rows = rows_aligned({value, out}) && small ? s.channels : 0;
   switch (rows) {
     case 16:
       launch_forward_rows<VT, GT, 16>(value, shapes, starts, loc, attn, out, s, st);

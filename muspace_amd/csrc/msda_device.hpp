@@ -178,6 +178,48 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// ------------------------------------------------------- buffer loads ---
+
+// Raw buffer loads over a tensor of `bytes` bytes: a 16-byte load at an
+// offset past the end returns zeros (hardware range check), which the row
+// kernels use for bilinear corners outside their level.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOobOffset = 0x80000000u;  // past the end of every buffer used here (< 2 GiB)
+constexpr uint32_t kBufferWord3 = 0x00020000u;  // raw, untyped 32-bit data
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), static_cast<int>(kBufferWord3));
+}
+
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+}
+
+// 16 raw bytes of channels -> floats
+__device__ __forceinline__ void decode16(float, u32x4 v, float (&o)[4]) {
+  o[0] = __uint_as_float(v.x);
+  o[1] = __uint_as_float(v.y);
+  o[2] = __uint_as_float(v.z);
+  o[3] = __uint_as_float(v.w);
+}
+__device__ __forceinline__ void decode16(bf16_t, u32x4 v, float (&o)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __uint_as_float(w[i] << 16);
+    o[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void decode16(__half, u32x4 v, float (&o)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[i] & 0xffffu)));
+    o[2 * i + 1] = __half2float(__ushort_as_half(static_cast<unsigned short>(w[i] >> 16)));
+  }
+}
+
 // --------------------------------------------------------------- staging ---
 
 // Copy level metadata into LDS. A level whose cells would fall outside

@@ -56,18 +56,34 @@ __device__ __forceinline__ Unit decode_unit(int u, const Shape &s) {
 
 // ------------------------------------------------------------- forward ---
 
+// Forward row kernel. Per step (a chunk of NS samples for each lane group),
+// lane i < NG*NS computes one sample's bilinear tap -- the four corner byte
+// offsets (kOobOffset for a corner outside the level) and the four weights
+// with the attention weight folded in -- into a wavefront-private LDS table;
+// then lane group g gathers the corner rows of its NS samples with 16-byte
+// buffer loads (out-of-range offsets read zeros) and accumulates. The next
+// step's geometry is loaded before the gathers are waited for (vmcnt counts
+// in issue order), and every load is unconditional (clamped indices): a load
+// inside a branch is waited for before the branch joins.
+// value_bytes < 2^31 (checked on the host) keeps every offset in 32 bits.
 template <typename VT, typename GT, int C, int NS>
 __global__ void __launch_bounds__(kBlock)
-    msda_forward_rows(const VT *__restrict__ value, const int64_t *__restrict__ shapes,
-                      const int64_t *__restrict__ starts, const GT *__restrict__ loc,
-                      const GT *__restrict__ attn, VT *__restrict__ out, Shape s, RowPlan plan) {
+    msda_forward_rows(const VT *__restrict__ value, uint32_t value_bytes,
+                      const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
+                      const GT *__restrict__ loc, const GT *__restrict__ attn,
+                      VT *__restrict__ out, Shape s, RowPlan plan) {
   constexpr int CPL = RowTraits<VT>::kCpl;
+  constexpr int VB = static_cast<int>(sizeof(VT));
   constexpr int KQ = C / CPL;
   constexpr int NG = kWave / KQ;
   static_assert(C % CPL == 0 && (KQ & (KQ - 1)) == 0 && KQ <= kWave, "bad row layout");
+  static_assert(NG * NS <= kWave, "one tap per lane");
 
   __shared__ Level lv[kMaxLevels];
+  __shared__ u32x4 tap_off[kBlock];
+  __shared__ float4 tap_w[kBlock];
   stage_levels(lv, shapes, starts, s);
+  const __amdgpu_buffer_rsrc_t vr = make_rsrc(value, value_bytes);
 
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
@@ -77,67 +93,99 @@ __global__ void __launch_bounds__(kBlock)
   const int gi = grp & (GU - 1);
   const int slot = grp >> plan.gu_log2;
   const int MC = s.heads * C;
+  // the sample this lane computes the tap of: sample tj of lane group tg
+  const int tg = min(lane / NS, NG - 1), tj = lane % NS;
+  const int tgi = tg & (GU - 1), tslot = tg >> plan.gu_log2;
+  u32x4 *my_off = tap_off + wave * kWave;
+  float4 *my_w = tap_w + wave * kWave;
 
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const int64_t wave_id = static_cast<int64_t>(lb) * (kBlock / kWave) + wave;
+  const int chunks = (s.lp + GU * NS - 1) / (GU * NS);
+  const int steps = plan.iters * chunks;
 
-  for (int it = 0; it < plan.iters; ++it) {
-    const int64_t u64 = (wave_id * plan.iters + it) * UW + slot;
-    const bool live = u64 < s.units;
+  // geometry of this lane's tap sample in step st
+  float lx, ly, a;
+  bool ok;
+  int sm;
+  uint32_t unit_base;  // byte offset of the tap unit's (b, head m) in value
+  auto load_geometry = [&](int st) {
+    const int it = st / chunks, s0 = (st % chunks) * GU * NS;
+    const int64_t u64 = (wave_id * plan.iters + it) * UW + tslot;
+    const bool live = st < steps && u64 < s.units && lane < NG * NS;
     const Unit U = decode_unit(live ? static_cast<int>(u64) : 0, s);
-    const VT *vbase = value + static_cast<size_t>(U.b) * s.spatial * MC + U.m * C + k * CPL;
-    const GT *lbase = loc + static_cast<size_t>(U.si) * s.lp * 2;
-    const GT *abase = attn + static_cast<size_t>(U.si) * s.lp;
+    const int smp = s0 + tgi + GU * tj;
+    ok = live && smp < s.lp;
+    sm = ok ? smp : 0;
+    const size_t o = static_cast<size_t>(U.si) * s.lp + sm;
+    lx = to_float(loc[2 * o]);
+    ly = to_float(loc[2 * o + 1]);
+    a = to_float(attn[o]);
+    unit_base = static_cast<uint32_t>((static_cast<size_t>(U.b) * s.spatial * MC + U.m * C) * VB);
+  };
+  load_geometry(0);
+  float acc[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
 
-    float acc[CPL];
+  for (int st = 0; st < steps; ++st) {
+    // A. this lane's tap into the wavefront's table
+    {
+      const Level L = lv[level_of_sample(sm, s)];
+      const Tap t = make_tap(lx, ly, L, ok);
+      const float ai = ok ? a : 0.0f;
+      const uint32_t row = static_cast<uint32_t>(MC * VB);
+      const uint32_t c00 = unit_base + static_cast<uint32_t>(L.start + t.cell00) * row;
+      const uint32_t c10 = c00 + static_cast<uint32_t>(L.w) * row;
+      u32x4 off;
+      off.x = t.y0ok && t.x0ok ? c00 : kOobOffset;
+      off.y = t.y0ok && t.x1ok ? c00 + row : kOobOffset;
+      off.z = t.y1ok && t.x0ok ? c10 : kOobOffset;
+      off.w = t.y1ok && t.x1ok ? c10 + row : kOobOffset;
+      my_off[lane] = off;
+      my_w[lane] = make_float4(ai * (t.wy0 * t.wx0), ai * (t.wy0 * t.wx1), ai * (t.wy1 * t.wx0),
+                               ai * (t.wy1 * t.wx1));
+    }
+    // B. gathers of this lane group's NS samples, then the next step's geometry
+    u32x4 raw[NS][4];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
-
-    for (int s0 = 0; s0 < s.lp; s0 += GU * NS) {
-      float w[NS][4];
-      float v[NS][4][CPL];
+    for (int j = 0; j < NS; ++j) {
+      const u32x4 off = my_off[grp * NS + j];
+      const uint32_t ch = static_cast<uint32_t>(k * 16);
+      raw[j][0] = buffer_load16(vr, off.x + ch);
+      raw[j][1] = buffer_load16(vr, off.y + ch);
+      raw[j][2] = buffer_load16(vr, off.z + ch);
+      raw[j][3] = buffer_load16(vr, off.w + ch);
+    }
+    load_geometry(st + 1);
+    // C. accumulate
 #pragma unroll
-      for (int i = 0; i < NS; ++i) {
-        const int smp = s0 + gi + GU * i;
-        const bool ok = live && smp < s.lp;
-        const int sm = ok ? smp : 0;
-        const Level L = lv[level_of_sample(sm, s)];
-        const float a = ok ? to_float(abase[sm]) : 0.0f;
-        const Tap t = make_tap(to_float(lbase[2 * sm]), to_float(lbase[2 * sm + 1]), L, ok);
-        w[i][0] = a * (t.wy0 * t.wx0);
-        w[i][1] = a * (t.wy0 * t.wx1);
-        w[i][2] = a * (t.wy1 * t.wx0);
-        w[i][3] = a * (t.wy1 * t.wx1);
-        const int c00 = (L.start + t.cell00) * MC;
-        const int c10 = c00 + L.w * MC;
-        const bool ok4[4] = {t.y0ok && t.x0ok, t.y0ok && t.x1ok, t.y1ok && t.x0ok,
-                             t.y1ok && t.x1ok};
-        const int off4[4] = {c00, c00 + MC, c10, c10 + MC};
+    for (int j = 0; j < NS; ++j) {
+      const float4 w = my_w[grp * NS + j];
+      float v0[CPL], v1[CPL], v2[CPL], v3[CPL];
+      decode16(VT(), raw[j][0], v0);
+      decode16(VT(), raw[j][1], v1);
+      decode16(VT(), raw[j][2], v2);
+      decode16(VT(), raw[j][3], v3);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          if (ok4[c]) {
-            load16(vbase + off4[c], v[i][c]);
-          } else {
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) v[i][c][j] = 0.0f;
-          }
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < NS; ++i) {
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-          acc[j] += w[i][0] * v[i][0][j] + w[i][1] * v[i][1][j] + w[i][2] * v[i][2][j] +
-                    w[i][3] * v[i][3][j];
-        }
+      for (int c = 0; c < CPL; ++c) {
+        acc[c] += w.x * v0[c] + w.y * v1[c] + w.z * v2[c] + w.w * v3[c];
       }
     }
-    // sum the GU groups of the unit (lane distance KQ, 2KQ, ...)
-    for (int off = KQ; off < KQ * GU; off <<= 1) {
+    // D. end of the unit: sum the GU groups (lane distance KQ, 2KQ, ...), store
+    if (st % chunks == chunks - 1) {
+      for (int off = KQ; off < KQ * GU; off <<= 1) {
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) acc[j] += __shfl_xor(acc[j], off, kWave);
+        for (int j = 0; j < CPL; ++j) acc[j] += __shfl_xor(acc[j], off, kWave);
+      }
+      const int64_t u64 = (wave_id * plan.iters + st / chunks) * UW + slot;
+      if (u64 < s.units && gi == 0) {
+        const Unit U = decode_unit(static_cast<int>(u64), s);
+        store16(out + static_cast<size_t>(U.si) * C + k * CPL, acc);
+      }
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
     }
-    if (live && gi == 0) store16(out + static_cast<size_t>(U.si) * C + k * CPL, acc);
   }
 }
 
