@@ -44,6 +44,28 @@ struct Unit {
   int b, m, si;
 };
 
+// Unit u, advanced in steps of `stride` units without divisions.
+struct UnitIter {
+  int b, m, q;
+  __device__ __forceinline__ void init(int64_t u, const Shape &s) {
+    q = static_cast<int>(u % s.queries);
+    const int64_t t = u / s.queries;
+    m = static_cast<int>(t % s.heads);
+    b = static_cast<int>(t / s.heads);
+  }
+  __device__ __forceinline__ void advance(int stride, const Shape &s) {
+    q += stride;
+    while (q >= s.queries) {  // at most stride / queries + 1 times
+      q -= s.queries;
+      if (++m == s.heads) {
+        m = 0;
+        ++b;
+      }
+    }
+  }
+  __device__ __forceinline__ int si(const Shape &s) const { return (b * s.queries + q) * s.heads + m; }
+};
+
 __device__ __forceinline__ Unit decode_unit(int u, const Shape &s) {
   const int q = u % s.queries;
   const int t = u / s.queries;
@@ -104,24 +126,31 @@ __global__ void __launch_bounds__(kBlock)
   const int chunks = (s.lp + GU * NS - 1) / (GU * NS);
   const int steps = plan.iters * chunks;
 
-  // geometry of this lane's tap sample in step st
+  // geometry of this lane's tap sample in step st; the tap unit and the
+  // output unit advance by UW units per wave iteration
+  const int64_t u_first = wave_id * plan.iters * UW;
+  UnitIter tu, ou;
+  tu.init(u_first + tslot, s);
+  ou.init(u_first + slot, s);
   float lx, ly, a;
   bool ok;
   int sm;
   uint32_t unit_base;  // byte offset of the tap unit's (b, head m) in value
   auto load_geometry = [&](int st) {
     const int it = st / chunks, s0 = (st % chunks) * GU * NS;
-    const int64_t u64 = (wave_id * plan.iters + it) * UW + tslot;
+    if (st > 0 && st % chunks == 0) tu.advance(UW, s);
+    const int64_t u64 = u_first + static_cast<int64_t>(it) * UW + tslot;
     const bool live = st < steps && u64 < s.units && lane < NG * NS;
-    const Unit U = decode_unit(live ? static_cast<int>(u64) : 0, s);
     const int smp = s0 + tgi + GU * tj;
     ok = live && smp < s.lp;
     sm = ok ? smp : 0;
-    const size_t o = static_cast<size_t>(U.si) * s.lp + sm;
+    const size_t o = live ? static_cast<size_t>(tu.si(s)) * s.lp + sm : 0;
     lx = to_float(loc[2 * o]);
     ly = to_float(loc[2 * o + 1]);
     a = to_float(attn[o]);
-    unit_base = static_cast<uint32_t>((static_cast<size_t>(U.b) * s.spatial * MC + U.m * C) * VB);
+    unit_base = live ? static_cast<uint32_t>(
+                           (static_cast<size_t>(tu.b) * s.spatial * MC + tu.m * C) * VB)
+                     : 0u;
   };
   load_geometry(0);
   float acc[CPL];
@@ -178,11 +207,11 @@ __global__ void __launch_bounds__(kBlock)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) acc[j] += __shfl_xor(acc[j], off, kWave);
       }
-      const int64_t u64 = (wave_id * plan.iters + st / chunks) * UW + slot;
+      const int64_t u64 = u_first + static_cast<int64_t>(st / chunks) * UW + slot;
       if (u64 < s.units && gi == 0) {
-        const Unit U = decode_unit(static_cast<int>(u64), s);
-        store16(out + static_cast<size_t>(U.si) * C + k * CPL, acc);
+        store16(out + static_cast<size_t>(ou.si(s)) * C + k * CPL, acc);
       }
+      ou.advance(UW, s);
 #pragma unroll
       for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
     }
