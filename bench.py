@@ -15,11 +15,11 @@ synthetic inputs resident in HBM before timing.
 value = effective GB/s = algorithmic bytes of fwd+bwd / measured time per step
 (byte model: every tensor once at its storage width; see muspace_amd/workloads.py).
 The roofline entry prices the dominant launch -- the backward entry point,
-one C-ABI call that runs four kernels (bin_count, bin_scan, bin_scatter,
-tile_backward) -- against the 8 TB/s HBM peak, from HIP events around each
-backward call in the timed region; `traffic` is the measured HBM bytes of
-those four kernels per call (rocprofv3 FETCH_SIZE/WRITE_SIZE, calibrated on a
-copy kernel) when profiles/traffic_c2_fp32.json holds them. cpu_baseline times the oracle (a CPU restatement of the reference's
+one C-ABI call that runs five kernels (bin_count, bin_scan, bin_scatter,
+tile_backward, grad_gather) -- against the 8 TB/s HBM peak, from HIP events
+around each backward call in the timed region; `traffic` is the measured HBM
+bytes of those five kernels per call (rocprofv3 FETCH_SIZE/WRITE_SIZE,
+calibrated on a copy kernel) from profiles/traffic_c2_fp32.json. cpu_baseline times the oracle (a CPU restatement of the reference's
 PyTorch path) on a query subset of the same workload.
 """
 
@@ -266,7 +266,7 @@ def main() -> int:
         "roofline": {
             "bound": "hbm",
             "kernel": "ms_deform_attn_backward (msda_bin_count, msda_bin_scan, "
-                      "msda_bin_scatter, msda_tile_backward<float,32>)",
+                      "msda_bin_scatter, msda_tile_backward<float,32>, msda_grad_gather)",
             "achieved": round(bwd_achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
