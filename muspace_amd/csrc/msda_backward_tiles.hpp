@@ -77,18 +77,18 @@ constexpr uint32_t kSplitBit = 0x80000000u;
 constexpr uint32_t kNoRecord = 0xffffffffu;  // sample with no corner inside its level
 constexpr uint32_t kTileIndexMask = 0xffffu;
 
-// Tile-kernel configuration per (value type, channels): tile edge T, batch
-// size K (records sorted together) and channels per lane CPL. The LDS holds
-// the value tile with its halo, four fp32 corner planes, K staged grad_out
-// rows, K sorted records, two id buffers and the position counts.
+// Tile-kernel configuration per (value type, channels): tile edge T and
+// batch size K (records sorted together); CPL channels per lane. The LDS
+// holds the value tile with its halo plus a zero row, four fp32 corner
+// planes, K sorted records and the position counts, offsets and order.
 template <typename VT, int C>
 struct TileCfg;
-template <> struct TileCfg<float, 16> { static constexpr int T = 14, K = 512, CPL = 4; };
-template <> struct TileCfg<float, 32> { static constexpr int T = 10, K = 512, CPL = 4; };
-template <> struct TileCfg<float, 64> { static constexpr int T = 7, K = 256, CPL = 4; };
-template <> struct TileCfg<bf16_t, 16> { static constexpr int T = 14, K = 512, CPL = 4; };
-template <> struct TileCfg<bf16_t, 32> { static constexpr int T = 12, K = 512, CPL = 4; };
-template <> struct TileCfg<bf16_t, 64> { static constexpr int T = 7, K = 512, CPL = 4; };
+template <> struct TileCfg<float, 16> { static constexpr int T = 16, K = 2048, CPL = 4; };
+template <> struct TileCfg<float, 32> { static constexpr int T = 12, K = 2048, CPL = 4; };
+template <> struct TileCfg<float, 64> { static constexpr int T = 8, K = 2048, CPL = 4; };
+template <> struct TileCfg<bf16_t, 16> { static constexpr int T = 16, K = 2048, CPL = 4; };
+template <> struct TileCfg<bf16_t, 32> { static constexpr int T = 13, K = 2048, CPL = 4; };
+template <> struct TileCfg<bf16_t, 64> { static constexpr int T = 9, K = 2048, CPL = 4; };
 template <> struct TileCfg<__half, 16> : TileCfg<bf16_t, 16> {};
 template <> struct TileCfg<__half, 32> : TileCfg<bf16_t, 32> {};
 template <> struct TileCfg<__half, 64> : TileCfg<bf16_t, 64> {};
@@ -98,9 +98,7 @@ __host__ __device__ constexpr size_t tile_lds_bytes() {
   constexpr int T = TileCfg<VT, C>::T, K = TileCfg<VT, C>::K, NPOS = (T + 1) * (T + 1);
   return static_cast<size_t>(NPOS + 1) * C * sizeof(VT) +  // value tile + halo, zero row
          static_cast<size_t>(4 * NPOS) * C * 4 +           // corner planes
-         static_cast<size_t>(K) * C * sizeof(VT) +         // staged grad_out rows
          static_cast<size_t>(K) * 16 +                     // sorted records
-         static_cast<size_t>(2 * K) * 4 +                  // record ids, two batches
          static_cast<size_t>(3 * NPOS) * 4 +               // position count, offset, order
          64 * 4 +                                          // count buckets
          static_cast<size_t>(C) * 4;                       // zero slot
@@ -249,7 +247,8 @@ __global__ void __launch_bounds__(kBinBlock)
     msda_bin_scan(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                   Shape s, BinPlan p, uint32_t *__restrict__ counts,
                   uint32_t *__restrict__ tile_start, uint32_t *__restrict__ item_total,
-                  Item *__restrict__ items, float *__restrict__ grad_value) {
+                  Item *__restrict__ items, uint32_t *__restrict__ zero_tiles,
+                  float *__restrict__ grad_value) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
   __shared__ uint32_t part[kBinBlock / kWave];
@@ -331,23 +330,30 @@ __global__ void __launch_bounds__(kBinBlock)
   }
   __syncthreads();
 
-  // non-boundary cells of empty and split tiles (boundary cells: bin_count)
-  const int MC = s.heads * C;
-  const size_t slab = static_cast<size_t>(b) * s.spatial * MC + m * C;
+  // empty and split tiles, whose non-boundary cells bin_scatter zeroes
+  // (boundary cells: bin_count); zero_tiles[slab] = {count, tile...}
+  uint32_t *zl = zero_tiles + static_cast<size_t>(bm) * (p.tile_bound + 1);
   const uint32_t nz = zero_count;
-  const bool listed = nz <= static_cast<uint32_t>(kZeroList);
-  for (uint32_t i = 0; i < (listed ? nz : static_cast<uint32_t>(nt)); ++i) {
-    const int t = listed ? static_cast<int>(zero_list[i]) : static_cast<int>(i);
-    if (!listed) {
-      const uint32_t n = ts[t + 1] - ts[t];
-      if (n != 0 && n <= rmax) continue;
+  if (nz <= static_cast<uint32_t>(kZeroList)) {
+    for (uint32_t i = threadIdx.x; i < nz; i += blockDim.x) zl[1 + i] = zero_list[i];
+    if (threadIdx.x == 0) zl[0] = nz;
+  } else if (threadIdx.x == 0) {
+    uint32_t n = 0;
+    for (int t = 0; t < nt; ++t) {
+      const uint32_t c = ts[t + 1] - ts[t];
+      if (c == 0 || c > rmax) zl[1 + n++] = static_cast<uint32_t>(t);
     }
-    const TileGeom g = tile_geom(t, T, ntc, base);
-    zero_tile_cells<C, T>(grad_value, slab, MC, lv[g.l], g, threadIdx.x, blockDim.x,
-                          [&](int r, int c) { return !boundary_cell(r, c, g); });
+    zl[0] = n;
   }
 
+  const int MC = s.heads * C;
+  const size_t slab = static_cast<size_t>(b) * s.spatial * MC + m * C;
   // value rows of this (b, m) that belong to no level get a zero gradient
+  // (none when the levels tile [0, spatial), the usual case: valid levels
+  // do not overlap, so covering `spatial` cells means covering them all)
+  int64_t covered_cells = 0;
+  for (int l = 0; l < s.levels; ++l) covered_cells += static_cast<int64_t>(lv[l].h) * lv[l].w;
+  if (covered_cells == s.spatial) return;
   for (int cell = threadIdx.x; cell < s.spatial; cell += blockDim.x) {
     bool covered = false;
     for (int l = 0; l < s.levels && !covered; ++l) {
@@ -364,12 +370,13 @@ __global__ void __launch_bounds__(kBinBlock)
 
 // ---------------------------------------------------------- 3. scatter ---
 
-template <typename GT, int T>
+template <typename GT, int C, int T>
 __global__ void __launch_bounds__(kBinBlock)
     msda_bin_scatter(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                      const GT *__restrict__ loc, const GT *__restrict__ attn, Shape s, BinPlan p,
-                     const uint32_t *__restrict__ counts, uint4 *__restrict__ records,
-                     uint32_t *__restrict__ rec_of_sample) {
+                     const uint32_t *__restrict__ counts, const uint32_t *__restrict__ zero_tiles,
+                     uint4 *__restrict__ records, uint32_t *__restrict__ rec_of_sample,
+                     float *__restrict__ grad_value) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
   extern __shared__ uint32_t cursor[];
@@ -386,22 +393,58 @@ __global__ void __launch_bounds__(kBinBlock)
   const int nq = min(p.chunk_q, s.queries - q0);
   uint4 *rec = records + static_cast<size_t>(bm) * p.rec_cap;
   const int lpp = 1 << p.lp_log2;
-  for (int i = threadIdx.x; i < nq * lpp; i += blockDim.x) {
-    const int q = q0 + (i >> p.lp_log2), smp = i & (lpp - 1);
-    if (smp >= s.lp) continue;
-    const size_t o = (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp;
-    const int l = level_of_sample(smp, s);
-    const float lx = to_float(loc[2 * o]), ly = to_float(loc[2 * o + 1]);
-    const Tap t = make_tap(lx, ly, lv[l], true);
-    if (!t.in) {
-      rec_of_sample[o] = kNoRecord;
-      continue;
+  const int total = nq * lpp;
+  // U samples per thread in flight: loads first (unconditional, clamped
+  // index), then the cursor atomics, then the stores
+  constexpr int U = 4;
+  for (int i0 = threadIdx.x; i0 < total; i0 += kBinBlock * U) {
+    float lx[U], ly[U], aw[U];
+    size_t o[U];
+    bool live[U];
+    int smp[U], q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * kBinBlock;
+      q[u] = q0 + (i >> p.lp_log2);
+      smp[u] = i & (lpp - 1);
+      live[u] = i < total && smp[u] < s.lp;
+      o[u] = live[u] ? (static_cast<size_t>(b * s.queries + q[u]) * s.heads + m) * s.lp + smp[u]
+                     : 0;
+      lx[u] = to_float(loc[2 * o[u]]);
+      ly[u] = to_float(loc[2 * o[u] + 1]);
+      aw[u] = to_float(attn[o[u]]);
     }
-    const uint32_t id = (static_cast<uint32_t>(q) << p.lp_log2) | static_cast<uint32_t>(smp);
-    const uint32_t at = atomicAdd(&cursor[primary_tile<T>(t, ntc[l], base[l])], 1u);
-    rec[at] = make_uint4(id, __float_as_uint(lx), __float_as_uint(ly),
-                         __float_as_uint(to_float(attn[o])));
-    rec_of_sample[o] = at;
+    uint32_t at[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int l = level_of_sample(live[u] ? smp[u] : 0, s);
+      const Tap t = make_tap(lx[u], ly[u], lv[l], live[u]);
+      at[u] = kNoRecord;
+      if (t.in) at[u] = atomicAdd(&cursor[primary_tile<T>(t, ntc[l], base[l])], 1u);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!live[u]) continue;
+      if (at[u] != kNoRecord) {
+        const uint32_t id =
+            (static_cast<uint32_t>(q[u]) << p.lp_log2) | static_cast<uint32_t>(smp[u]);
+        rec[at[u]] = make_uint4(id, __float_as_uint(lx[u]), __float_as_uint(ly[u]),
+                                __float_as_uint(aw[u]));
+      }
+      rec_of_sample[o[u]] = at[u];
+    }
+  }
+
+  // non-boundary cells of the slab's empty and split tiles listed by
+  // bin_scan: tiles ch, ch + chunks, ... of the list
+  const uint32_t *zl = zero_tiles + static_cast<size_t>(bm) * (p.tile_bound + 1);
+  const uint32_t nz = zl[0];
+  const int MC = s.heads * C;
+  const size_t slab = static_cast<size_t>(b) * s.spatial * MC + m * C;
+  for (uint32_t z = ch; z < nz; z += p.chunks) {
+    const TileGeom g = tile_geom(static_cast<int>(zl[1 + z]), T, ntc, base);
+    zero_tile_cells<C, T>(grad_value, slab, MC, lv[g.l], g, threadIdx.x, blockDim.x,
+                          [&](int r, int c) { return !boundary_cell(r, c, g); });
   }
 }
 
@@ -423,19 +466,27 @@ __device__ __forceinline__ uint32_t item_batches(const Item &d) {
 
 // One work item = records [r0, r1) of a tile of T x T value cells. The
 // records are processed in batches of K: counting-sorted by top-left corner
-// position ((T+1)^2 positions, [-1, T-1]^2 in the tile frame), then lane
-// group g owns positions g, g + NG, ... and accumulates, in registers, the
-// four corner sums S_p[d] = sum_r w_d(r) * attn(r) * grad_out[q(r)] of each
-// of them; S_p[d] is added to slot p of corner plane d (no other group writes
-// it). At the end of the item, cell (r, c) sums slot (r - dy, c - dx) of
-// plane (dy, dx). Per record, the owner group also produces the attention
-// and location gradients from the LDS value tile:
-//   D_d = grad_out . v_d (corner value rows), grad_attn = sum_d w_d D_d,
+// position ((T+1)^2 positions, [-1, T-1]^2 in the tile frame) in LDS; lane
+// group g then owns positions of rank g, g + NG, ... in decreasing-count
+// order and accumulates, in registers, the four corner sums
+// S_p[d] = sum_r w_d(r) * attn(r) * grad_out[q(r)] of each; S_p[d] is added
+// to slot p of corner plane d (no other group writes it). At the end of the
+// item, cell (r, c) sums slot (r - dy, c - dx) of plane (dy, dx). Per record
+// the owner group also computes the four corner dot products
+// D_d = grad_out . v_d from the LDS value tile, from which one thread per
+// record forms the attention and location gradients:
+//   grad_attn = sum_d w_d D_d,
 //   grad_ix = attn * (wy0 (D1 - D0) + wy1 (D3 - D2)),
 //   grad_iy = attn * (wx0 (D2 - D0) + wx1 (D3 - D1)),
-//   grad_loc = (grad_ix * W, grad_iy * H)   (d ix / d loc_x = W)
-// which is grid_sample's bilinear backward (zeros padding) regrouped by
-// corner.
+//   grad_loc = (grad_ix * W, grad_iy * H)   (d ix / d loc_x = W),
+// grid_sample's bilinear backward (zeros padding) regrouped by corner; they
+// are stored over the record's own (consumed) slot for msda_grad_gather.
+//
+// Memory order: gfx950 counts loads and stores in one in-order vmcnt, so the
+// owner loop (which loads grad_out rows one record ahead) waits for every
+// earlier memory operation. The next batch's records and value tile are
+// therefore issued first thing in a batch, and the stores of finished work
+// right after them, well before the owner phase.
 template <typename VT, int C>
 __global__ void __launch_bounds__(kTileBlock)
     msda_tile_backward(const VT *__restrict__ value, const int64_t *__restrict__ shapes,
@@ -448,18 +499,12 @@ __global__ void __launch_bounds__(kTileBlock)
   constexpr int TV = T + 1, NPOS = TV * TV;
   constexpr int KQ = C / CPL;          // lanes per group
   constexpr int NG = kTileBlock / KQ;  // lane groups
-  constexpr int GROWS = K / NG;        // grad_out rows staged per group and batch
   constexpr int VB = static_cast<int>(sizeof(VT));
   constexpr int UPV = C * VB / 16;     // 16-byte units per value row
-  constexpr int LANE_B = CPL * VB;     // bytes per lane and grad_out row
-  // native vector types (HIP's uint4 is a union wrapper that keeps arrays of
-  // it in scratch memory)
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-  using LaneUnit = typename std::conditional<LANE_B == 16, u32x4, u32x2>::type;
+  constexpr int VPT = (NPOS * UPV + kTileBlock - 1) / kTileBlock;  // value units per thread
+  constexpr int RPT = K / kTileBlock;  // records per thread
   static_assert(CPL == 4 && (KQ & (KQ - 1)) == 0 && KQ <= kWave, "bad lane layout");
-  static_assert(NPOS * UPV <= kTileBlock, "value tile: one 16-byte unit per thread");
-  static_assert(K <= kTileBlock && K % NG == 0 && NPOS <= kTileBlock, "bad batch size");
+  static_assert(K % kTileBlock == 0 && NPOS <= kTileBlock, "bad batch size");
   static_assert(tile_lds_bytes<VT, C>() + 3400 <= kTileLdsLimit, "tile LDS budget");
 
   __shared__ Level lv[kMaxLevels];
@@ -467,10 +512,8 @@ __global__ void __launch_bounds__(kTileBlock)
   extern __shared__ __align__(16) unsigned char lds[];
   VT *vt = reinterpret_cast<VT *>(lds);  // NPOS cells + one zero row
   float *planes = reinterpret_cast<float *>(lds + static_cast<size_t>(NPOS + 1) * C * VB);
-  VT *gst = reinterpret_cast<VT *>(planes + 4 * NPOS * C);
-  uint4 *stash = reinterpret_cast<uint4 *>(gst + K * C);
-  uint32_t *ids = reinterpret_cast<uint32_t *>(stash + K);  // [2][K]
-  uint32_t *pcount = ids + 2 * K;
+  uint4 *stash = reinterpret_cast<uint4 *>(planes + 4 * NPOS * C);
+  uint32_t *pcount = reinterpret_cast<uint32_t *>(stash + K);
   uint32_t *poff = pcount + NPOS;
   uint32_t *order = poff + NPOS;
   uint32_t *bucket = order + NPOS;                         // [64]
@@ -496,8 +539,8 @@ __global__ void __launch_bounds__(kTileBlock)
     return d;
   };
 
-  // cursors of batches b (c0), b + 1 (c1) and b + 2 (c2); `pre` is the
-  // descriptor of the item after c2's
+  // cursors of batches b (c0) and b + 1 (c1); `pre` is the descriptor of the
+  // item after c1's
   BatchCursor c0;
   c0.n = 0;
   c0.k = 0;
@@ -520,68 +563,50 @@ __global__ void __launch_bounds__(kTileBlock)
     return r;
   };
   BatchCursor c1 = advance(c0);
-  BatchCursor c2 = advance(c1);
 
   auto batch_range = [&](const BatchCursor &c, uint32_t &s0, uint32_t &s1) {
     s0 = c.d.r0 + c.k * K;
     s1 = min(c.d.r1, s0 + K);
   };
-  // Loads below are issued unconditionally (a clamped, always valid address
-  // when there is nothing to load) so that no branch separates a prefetch
-  // from the code that consumes it a batch later.
-  auto load_record = [&](const BatchCursor &c) {
+  auto rec_base = [&](const Item &d) {
+    return static_cast<size_t>(d.b * s.heads + d.m) * p.rec_cap;
+  };
+  // loads are issued unconditionally (clamped, always valid addresses): a
+  // load inside a branch is waited for before the branch joins
+  auto load_record = [&](const BatchCursor &c, int u) {
     uint32_t s0, s1;
     batch_range(c, s0, s1);
-    const bool ok = c.valid && tid < K && s0 + tid < s1;
-    const size_t at =
-        ok ? static_cast<size_t>(c.d.b * s.heads + c.d.m) * p.rec_cap + s0 + tid : 0;
+    const uint32_t i = s0 + tid + u * kTileBlock;
+    const size_t at = c.valid && i < s1 ? rec_base(c.d) + i : 0;
     return records[at];
   };
-  auto geom = [&](const BatchCursor &c) {
-    return item_geom(c.d);
-  };
+  auto geom = [&](const BatchCursor &c) { return item_geom(c.d); };
   auto slab_offset = [&](const Item &d) {
     return static_cast<size_t>(d.b) * s.spatial * MC + d.m * C;
   };
-  // source of this thread's 16-byte unit of the value tile (cells [0, T]^2)
-  // of c's item; `ok` false for cells outside the level (stored as zeros)
-  auto value_unit_src = [&](const BatchCursor &c, bool &ok) {
+  // source of 16-byte unit v of the value tile (cells [0, T]^2) of c's item;
+  // `ok` false for units past the tile or cells outside the level (stored as
+  // zeros)
+  auto value_unit_src = [&](const BatchCursor &c, int v, bool &ok) {
     const TileGeom g = geom(c);
     const Level L = lv[g.l];
-    const int u = tid < NPOS * UPV ? tid : 0;
+    const int unit = tid + v * kTileBlock;
+    const int u = unit < NPOS * UPV ? unit : 0;
     const int cell = u / UPV, kk = u % UPV;
     const int y = g.y_lo + cell / TV, x = g.x_lo + cell % TV;
-    ok = c.valid && tid < NPOS * UPV && y < L.h && x < L.w;
+    ok = c.valid && unit < NPOS * UPV && y < L.h && x < L.w;
     const size_t at =
         ok ? slab_offset(c.d) + static_cast<size_t>(L.start + y * L.w + x) * MC : 0;
     return reinterpret_cast<const uint4 *>(value + at) + (ok ? kk : 0);
   };
-  // source of row grp + j * NG of c's batch of grad_out rows, in record
-  // order (record ids read from bid; rows past the batch read row 0)
-  auto grow_src = [&](const BatchCursor &c, const uint32_t *bid, int j) {
-    uint32_t s0, s1;
-    batch_range(c, s0, s1);
-    const int ns = c.valid ? static_cast<int>(s1 - s0) : 0;
-    const int b = static_cast<int>(c.d.b), m = static_cast<int>(c.d.m);
-    const int t = grp + j * NG;
-    const int q = t < ns ? static_cast<int>(bid[t] >> p.lp_log2) : 0;
-    return reinterpret_cast<const LaneUnit *>(
-        grad_out + ((static_cast<size_t>(b) * s.queries + q) * s.heads + m) * C + k * CPL);
-  };
-  const uint32_t smask = (1u << p.lp_log2) - 1u;
-  // location and weight gradients of record t (batch order) of a finished
-  // batch, from its sorted slot (stash[slot] = {t, wx1, wy1, attn}) and the
-  // D_0..D_3 the owner left at the start of grad_out row t
-  auto finish_record = [&](int t, uint32_t slot, const Level &Lf, float &ga, float &gx,
-                           float &gy) {
-    const uint4 e = stash[slot];
-    const float4 D = *reinterpret_cast<const float4 *>(gst + t * C);
-    const float wx1 = __uint_as_float(e.y), wy1 = __uint_as_float(e.z);
-    const float a = __uint_as_float(e.w);
-    const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
-    ga = wy0 * (wx0 * D.x + wx1 * D.y) + wy1 * (wx0 * D.z + wx1 * D.w);
-    gx = a * (wy0 * (D.y - D.x) + wy1 * (D.w - D.z)) * Lf.fw;
-    gy = a * (wx0 * (D.z - D.x) + wx1 * (D.w - D.y)) * Lf.fh;
+  auto store_value_units = [&](const uint4 (&u)[VPT], const bool (&ok)[VPT]) {
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+      const int unit = tid + v * kTileBlock;
+      if (unit < NPOS * UPV) {
+        reinterpret_cast<uint4 *>(vt)[unit] = ok[v] ? u[v] : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
   };
   // cell sums of a finished item's corner planes to grad_value; every plane
   // slot that maps to a cell of [0, T]^2 is read once and zeroed (slots that
@@ -614,15 +639,16 @@ __global__ void __launch_bounds__(kTileBlock)
     }
   };
 
-  // prologue: batch 0's records, value tile and grad_out rows
-  uint4 r_cur = load_record(c0);
-  uint4 r_next = load_record(c1);
+  // prologue: batch 0's records and value tile
+  uint4 r_cur[RPT];
+#pragma unroll
+  for (int u = 0; u < RPT; ++u) r_cur[u] = load_record(c0, u);
   {
-    bool ok0;
-    const uint4 u = *value_unit_src(c0, ok0);
-    if (tid < NPOS * UPV) {
-      reinterpret_cast<uint4 *>(vt)[tid] = ok0 ? u : make_uint4(0u, 0u, 0u, 0u);
-    }
+    uint4 u0[VPT];
+    bool ok0[VPT];
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) u0[v] = *value_unit_src(c0, v, ok0[v]);
+    store_value_units(u0, ok0);
   }
   if (tid < UPV) reinterpret_cast<uint4 *>(vt + NPOS * C)[tid] = make_uint4(0u, 0u, 0u, 0u);
   if (tid < C) dummy[tid] = 0.0f;
@@ -630,22 +656,16 @@ __global__ void __launch_bounds__(kTileBlock)
     reinterpret_cast<float4 *>(planes)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
   if (tid < NPOS) pcount[tid] = 0;
-  if (tid < K) ids[tid] = r_cur.x;
   __syncthreads();
-  LaneUnit gregs[GROWS];
-#pragma unroll
-  for (int j = 0; j < GROWS; ++j) gregs[j] = *grow_src(c0, ids, j);
 
-  // the previous batch's location/weight gradients of this thread's record,
-  // stored over that (consumed) record during the next batch
+  // this thread's finished records of the previous batch: result and slot
   int ns_prev = 0;
-  size_t f_at = 0;
-  float f_ga = 0.0f, f_gx = 0.0f, f_gy = 0.0f;
-  bool wb_pending = false;  // the previous batch finished an item
-  Item wb_item{0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-  for (uint32_t bi = 0; c0.valid; ++bi) {
-    const uint32_t *ids_cur = ids + (bi & 1) * K;
-    uint32_t *ids_nxt = ids + ((bi + 1) & 1) * K;
+  size_t f_base = 0;
+  uint32_t f_s0 = 0;
+  float f_ga[RPT], f_gx[RPT], f_gy[RPT];
+  const uint32_t smask = (1u << p.lp_log2) - 1u;
+  (void)smask;
+  for (;;) {
     const TileGeom g0 = geom(c0);
     const Level L = lv[g0.l];
     uint32_t s0, s1;
@@ -653,34 +673,44 @@ __global__ void __launch_bounds__(kTileBlock)
     const int ns = static_cast<int>(s1 - s0);
     const bool last_of_item = c0.k + 1 == item_batches<K>(c0.d);
     const bool next_new_item = c1.valid && c1.k == 0;
+    const int b0 = static_cast<int>(c0.d.b), m0 = static_cast<int>(c0.d.m);
 
-    // A. sort keys of this batch; its grad_out rows into LDS; the next
-    // batch's ids; prefetch the batch after next and the next value tile;
-    // then the previous batch's gradient stores (after the waits above)
-    int pos = -1;
-    uint32_t rank = 0;
-    uint4 entry = make_uint4(0u, 0u, 0u, 0u);
-    if (tid < ns) {
-      const Tap t = make_tap(__uint_as_float(r_cur.y), __uint_as_float(r_cur.z), L, true);
-      const int py = t.y0 - g0.y_lo + 1, px = t.x0 - g0.x_lo + 1;
-      if (t.in && py >= 0 && py < TV && px >= 0 && px < TV) {  // always, for binned records
-        pos = py * TV + px;
-        entry = make_uint4(static_cast<uint32_t>(tid), __float_as_uint(t.wx1),
-                           __float_as_uint(t.wy1), r_cur.w);
-        rank = atomicAdd(&pcount[pos], 1u);
+    // A. next batch's records and value tile first; then the previous
+    // batch's results; then this batch's sort keys
+    uint4 r_next[RPT];
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) r_next[u] = load_record(c1, u);
+    uint4 v_next[VPT];
+    bool v_ok[VPT];
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) v_next[v] = *value_unit_src(c1, v, v_ok[v]);
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+      const int i = tid + u * kTileBlock;
+      if (i < ns_prev) {
+        records[f_base + f_s0 + i] = make_uint4(__float_as_uint(f_ga[u]), __float_as_uint(f_gx[u]),
+                                                __float_as_uint(f_gy[u]), 0u);
       }
     }
+    int pos[RPT];
+    uint32_t rank[RPT];
+    uint4 entry[RPT];
+    float my_wx1[RPT], my_wy1[RPT], my_a[RPT];
 #pragma unroll
-    for (int j = 0; j < GROWS; ++j) {
-      *reinterpret_cast<LaneUnit *>(gst + (grp + j * NG) * C + k * CPL) = gregs[j];
-    }
-    if (tid < K) ids_nxt[tid] = r_next.x;
-    const uint4 r_after = load_record(c2);
-    bool v_ok;
-    const uint4 v_next = *value_unit_src(c1, v_ok);
-    if (tid < ns_prev) {
-      records[f_at] = make_uint4(__float_as_uint(f_ga), __float_as_uint(f_gx),
-                                 __float_as_uint(f_gy), 0u);
+    for (int u = 0; u < RPT; ++u) {
+      const int i = tid + u * kTileBlock;
+      pos[u] = -1;
+      rank[u] = 0;
+      const Tap t = make_tap(__uint_as_float(r_cur[u].y), __uint_as_float(r_cur[u].z), L, i < ns);
+      const int py = t.y0 - g0.y_lo + 1, px = t.x0 - g0.x_lo + 1;
+      my_wx1[u] = t.wx1;
+      my_wy1[u] = t.wy1;
+      my_a[u] = __uint_as_float(r_cur[u].w);
+      entry[u] = make_uint4(r_cur[u].x, __float_as_uint(t.wx1), __float_as_uint(t.wy1), r_cur[u].w);
+      if (t.in && py >= 0 && py < TV && px >= 0 && px < TV) {  // always, for binned records
+        pos[u] = py * TV + px;
+        rank[u] = atomicAdd(&pcount[pos[u]], 1u);
+      }
     }
     __syncthreads();
 
@@ -717,21 +747,21 @@ __global__ void __launch_bounds__(kTileBlock)
     __syncthreads();
 
     // C. records in position order
-    uint32_t my_slot = 0;
-    if (pos >= 0) {
-      my_slot = poff[pos] + rank;
-      stash[my_slot] = entry;
+    uint32_t my_slot[RPT];
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+      my_slot[u] = 0;
+      if (pos[u] >= 0) {
+        my_slot[u] = poff[pos[u]] + rank[u];
+        stash[my_slot[u]] = entry[u];
+      }
     }
     __syncthreads();
 
-    // D. next batch's grad_out rows in flight; write back the item the
-    // previous batch finished; then reduce this batch
-#pragma unroll
-    for (int j = 0; j < GROWS; ++j) gregs[j] = *grow_src(c1, ids_nxt, j);
-    if (wb_pending) {
-      write_back(wb_item);
-      __syncthreads();
-    }
+    // D. owners: lane group grp takes ranks grp, grp + NG, ...
+    const VT *gbase =
+        grad_out + (static_cast<size_t>(b0) * s.queries * s.heads + m0) * C + k * CPL;
+    const size_t q_stride = static_cast<size_t>(s.heads) * C;
 #pragma unroll 1
     for (int i = grp; i < NPOS; i += NG) {
       const int p_id = static_cast<int>(order[i]);
@@ -740,30 +770,29 @@ __global__ void __launch_bounds__(kTileBlock)
       const uint32_t first = poff[p_id];
       const int py = p_id / TV - 1, px = p_id % TV - 1;  // tile frame, >= -1
       // corner value rows (row -1 or column -1: the zero row after the tile)
-      const VT *vrow[4];
+      float v[4][CPL];
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         const int cy = py + (d >> 1), cx = px + (d & 1);
-        vrow[d] = vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * C : NPOS * C) + k * CPL;
+        load4ch(vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * C : NPOS * C) + k * CPL, v[d]);
       }
-      float v[4][CPL];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) load4ch(vrow[d], v[d]);
       float acc[4][CPL];
 #pragma unroll
       for (int d = 0; d < 4; ++d)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) acc[d][j] = 0.0f;
       uint4 e = stash[first];
+      float gv[CPL];
+      load4ch(gbase + (e.x >> p.lp_log2) * q_stride, gv);
       for (uint32_t r = 0; r < n; ++r) {
+        // the next record and its grad_out row, one iteration ahead
         const uint4 e_next = stash[first + min(r + 1, n - 1)];
-        const int t = static_cast<int>(e.x);
+        float g_next[CPL];
+        load4ch(gbase + (e_next.x >> p.lp_log2) * q_stride, g_next);
         const float wx1 = __uint_as_float(e.y), wy1 = __uint_as_float(e.z);
         const float a = __uint_as_float(e.w);
         const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
         const float wa[4] = {wy0 * wx0 * a, wy0 * wx1 * a, wy1 * wx0 * a, wy1 * wx1 * a};
-        float gv[CPL];
-        load4ch(gst + t * C + k * CPL, gv);
         float D[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -775,10 +804,14 @@ __global__ void __launch_bounds__(kTileBlock)
           }
           D[d] = group_sum<KQ>(dd);
         }
-        // D_0..D_3 replace the start of grad_out row t (read by this group
-        // alone, above); the gradients are finished per record in E
-        if (k == 0) *reinterpret_cast<float4 *>(gst + t * C) = make_float4(D[0], D[1], D[2], D[3]);
+        // D_0..D_3 replace the consumed record (read by this group alone)
+        if (k == 0) {
+          stash[first + r] = make_uint4(__float_as_uint(D[0]), __float_as_uint(D[1]),
+                                        __float_as_uint(D[2]), __float_as_uint(D[3]));
+        }
         e = e_next;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) gv[j] = g_next[j];
       }
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
@@ -793,31 +826,45 @@ __global__ void __launch_bounds__(kTileBlock)
     }
     __syncthreads();
 
-    // E. this batch's location/weight gradients (stored in the next A),
-    // position counts reset, next value tile staged
-    if (tid < ns) {
-      finish_record(tid, my_slot, L, f_ga, f_gx, f_gy);
-      f_at = static_cast<size_t>(c0.d.b * s.heads + c0.d.m) * p.rec_cap + s0 + tid;
-    }
-    if (tid < NPOS) pcount[tid] = 0;
-    if (next_new_item && tid < NPOS * UPV) {
-      reinterpret_cast<uint4 *>(vt)[tid] = v_ok ? v_next : make_uint4(0u, 0u, 0u, 0u);
+    // E. this batch's location/weight gradients (stored during the next
+    // batch), position counts reset, a finished item written back, the next
+    // value tile staged
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+      const int i = tid + u * kTileBlock;
+      f_ga[u] = f_gx[u] = f_gy[u] = 0.0f;
+      if (i < ns) {
+        const uint4 Dr = stash[my_slot[u]];
+        const float D0 = __uint_as_float(Dr.x), D1 = __uint_as_float(Dr.y);
+        const float D2 = __uint_as_float(Dr.z), D3 = __uint_as_float(Dr.w);
+        const float wx1 = my_wx1[u], wy1 = my_wy1[u], a = my_a[u];
+        const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
+        f_ga[u] = wy0 * (wx0 * D0 + wx1 * D1) + wy1 * (wx0 * D2 + wx1 * D3);
+        f_gx[u] = a * (wy0 * (D1 - D0) + wy1 * (D3 - D2)) * L.fw;
+        f_gy[u] = a * (wx0 * (D2 - D0) + wx1 * (D3 - D1)) * L.fh;
+      }
     }
     ns_prev = ns;
-    wb_pending = last_of_item;
-    wb_item = c0.d;
-    r_cur = r_next;
-    r_next = r_after;
+    f_base = rec_base(c0.d);
+    f_s0 = s0;
+    if (tid < NPOS) pcount[tid] = 0;
+    if (last_of_item) write_back(c0.d);
+    if (next_new_item) store_value_units(v_next, v_ok);
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) r_cur[u] = r_next[u];
     c0 = c1;
-    c1 = c2;
-    c2 = advance(c2);
+    c1 = advance(c1);
     __syncthreads();
+    if (!c0.valid) break;
   }
-  if (tid < ns_prev) {
-    records[f_at] = make_uint4(__float_as_uint(f_ga), __float_as_uint(f_gx),
-                               __float_as_uint(f_gy), 0u);
+#pragma unroll
+  for (int u = 0; u < RPT; ++u) {
+    const int i = tid + u * kTileBlock;
+    if (i < ns_prev) {
+      records[f_base + f_s0 + i] = make_uint4(__float_as_uint(f_ga[u]), __float_as_uint(f_gx[u]),
+                                              __float_as_uint(f_gy[u]), 0u);
+    }
   }
-  if (wb_pending) write_back(wb_item);
 }
 
 // -------------------------------------------------------------- 5. gather ---

@@ -352,7 +352,7 @@ int tile_grid() {
 // Scratch layout of the tile-owned backward.
 struct TileWorkspace {
   msda::BinPlan plan;
-  size_t counts, tile_start, records, rec_of_sample, items, item_total, bytes;
+  size_t counts, tile_start, zero_tiles, records, rec_of_sample, items, item_total, bytes;
 };
 
 bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w) {
@@ -388,6 +388,7 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   };
   w.counts = take(static_cast<size_t>(bm) * p.chunks * p.tile_bound * 4);
   w.tile_start = take(static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
+  w.zero_tiles = take(static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
   w.records = take(static_cast<size_t>(bm) * p.rec_cap * 16);
   w.rec_of_sample = take(static_cast<size_t>(bm) * p.rec_cap * 4);
   w.items = take(static_cast<size_t>(p.item_cap) * sizeof(msda::Item));
@@ -405,6 +406,7 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + w.counts);
   uint32_t *tile_start = reinterpret_cast<uint32_t *>(ws + w.tile_start);
+  uint32_t *zero_tiles = reinterpret_cast<uint32_t *>(ws + w.zero_tiles);
   uint4 *records = reinterpret_cast<uint4 *>(ws + w.records);
   uint32_t *rec_of_sample = reinterpret_cast<uint32_t *>(ws + w.rec_of_sample);
   msda::Item *items = reinterpret_cast<msda::Item *>(ws + w.items);
@@ -418,7 +420,7 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4;
 
   auto count = msda::msda_bin_count<GT, C, T>;
-  auto scatter = msda::msda_bin_scatter<GT, T>;
+  auto scatter = msda::msda_bin_scatter<GT, C, T>;
   auto tile = msda::msda_tile_backward<VT, C>;
   constexpr size_t tile_bytes = msda::tile_lds_bytes<VT, C>();
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(count),
@@ -430,10 +432,10 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
 
   count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts,
                                                              item_total, gv);
-  msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(shapes, starts, s, p, counts,
-                                                            tile_start, item_total, items, gv);
-  scatter<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, aw, s, p,
-                                                               counts, records, rec_of_sample);
+  msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
+      shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
+  scatter<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(
+      shapes, starts, lc, aw, s, p, counts, zero_tiles, records, rec_of_sample, gv);
   tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, shapes, starts, go, records, items,
                                                           item_total, s, p, gv);
   const int per_slab = static_cast<int>((p.rec_cap + msda::kBinBlock - 1) / msda::kBinBlock);
