@@ -761,7 +761,7 @@ __global__ void __launch_bounds__(kTileBlock)
     // D. owners: lane group grp takes ranks grp, grp + NG, ...
     const VT *gbase =
         grad_out + (static_cast<size_t>(b0) * s.queries * s.heads + m0) * C + k * CPL;
-    const size_t q_stride = static_cast<size_t>(s.heads) * C;
+    const uint32_t q_stride = static_cast<uint32_t>(s.heads * C);  // grad_out row stride
 #pragma unroll 1
     for (int i = grp; i < NPOS; i += NG) {
       const int p_id = static_cast<int>(order[i]);
@@ -781,18 +781,18 @@ __global__ void __launch_bounds__(kTileBlock)
       for (int d = 0; d < 4; ++d)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) acc[d][j] = 0.0f;
-      uint4 e = stash[first];
-      float gv[CPL];
-      load4ch(gbase + (e.x >> p.lp_log2) * q_stride, gv);
-      for (uint32_t r = 0; r < n; ++r) {
-        // the next record and its grad_out row, one iteration ahead
-        const uint4 e_next = stash[first + min(r + 1, n - 1)];
-        float g_next[CPL];
-        load4ch(gbase + (e_next.x >> p.lp_log2) * q_stride, g_next);
+      // records in two register sets A and B, each refilled as soon as it is
+      // consumed: every wait for a grad_out row leaves the other in flight
+      auto grow = [&](uint32_t id) {
+        const uint32_t q = min(id >> p.lp_log2, static_cast<uint32_t>(s.queries - 1));
+        return gbase + static_cast<uint32_t>(q * q_stride);
+      };
+      auto one_record = [&](const u32x4 &e, const float (&gv)[CPL], uint32_t slot) {
         const float wx1 = __uint_as_float(e.y), wy1 = __uint_as_float(e.z);
         const float a = __uint_as_float(e.w);
-        const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
-        const float wa[4] = {wy0 * wx0 * a, wy0 * wx1 * a, wy1 * wx0 * a, wy1 * wx1 * a};
+        const float ay0 = (1.0f - wy1) * a, ay1 = wy1 * a;
+        const float wx0 = 1.0f - wx1;
+        const float wa[4] = {ay0 * wx0, ay0 * wx1, ay1 * wx0, ay1 * wx1};
         float D[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -806,12 +806,27 @@ __global__ void __launch_bounds__(kTileBlock)
         }
         // D_0..D_3 replace the consumed record (read by this group alone)
         if (k == 0) {
-          stash[first + r] = make_uint4(__float_as_uint(D[0]), __float_as_uint(D[1]),
-                                        __float_as_uint(D[2]), __float_as_uint(D[3]));
+          stash[slot] = make_uint4(__float_as_uint(D[0]), __float_as_uint(D[1]),
+                                   __float_as_uint(D[2]), __float_as_uint(D[3]));
         }
-        e = e_next;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) gv[j] = g_next[j];
+      };
+      // native vector registers (HIP's uint4 under a select lands in scratch)
+      const u32x4 *vstash = reinterpret_cast<const u32x4 *>(stash);
+      u32x4 eA = vstash[first], eB = vstash[first + min(1u, n - 1)];
+      float gA[CPL], gB[CPL];
+      load4ch(grow(eA.x), gA);
+      load4ch(grow(eB.x), gB);
+      // Past the end of the list a set keeps its (consumed) record: a slot
+      // already processed holds D values, not a record id.
+      for (uint32_t r = 0; r < n; r += 2) {
+        one_record(eA, gA, first + r);
+        const u32x4 tA = vstash[first + min(r + 2, n - 1)];
+        eA = r + 2 < n ? tA : eA;
+        load4ch(grow(eA.x), gA);
+        if (r + 1 < n) one_record(eB, gB, first + r + 1);
+        const u32x4 tB = vstash[first + min(r + 3, n - 1)];
+        eB = r + 3 < n ? tB : eB;
+        load4ch(grow(eB.x), gB);
       }
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
