@@ -48,7 +48,7 @@
 
 namespace msda {
 
-constexpr int kTileBlock = 1024;         // tile kernel workgroup (16 wavefronts)
+constexpr int kTileBlock = 512;          // tile kernel workgroup (8 wavefronts)
 constexpr int kBinBlock = 256;           // binning workgroup
 constexpr int kMaxTilesPerSlab = 16384;  // LDS histogram of the binning kernels
 constexpr int kZeroList = 2048;          // tiles listed for zeroing per slab
@@ -83,12 +83,12 @@ constexpr uint32_t kTileIndexMask = 0xffffu;
 // planes, K sorted records and the position counts, offsets and order.
 template <typename VT, int C>
 struct TileCfg;
-template <> struct TileCfg<float, 16> { static constexpr int T = 16, K = 2048, CPL = 4; };
-template <> struct TileCfg<float, 32> { static constexpr int T = 12, K = 2048, CPL = 4; };
-template <> struct TileCfg<float, 64> { static constexpr int T = 8, K = 2048, CPL = 4; };
-template <> struct TileCfg<bf16_t, 16> { static constexpr int T = 16, K = 2048, CPL = 4; };
-template <> struct TileCfg<bf16_t, 32> { static constexpr int T = 13, K = 2048, CPL = 4; };
-template <> struct TileCfg<bf16_t, 64> { static constexpr int T = 9, K = 2048, CPL = 4; };
+template <> struct TileCfg<float, 16> { static constexpr int T = 16, K = 2048, CPL = 8; };
+template <> struct TileCfg<float, 32> { static constexpr int T = 12, K = 2048, CPL = 8; };
+template <> struct TileCfg<float, 64> { static constexpr int T = 8, K = 2048, CPL = 8; };
+template <> struct TileCfg<bf16_t, 16> { static constexpr int T = 16, K = 2048, CPL = 8; };
+template <> struct TileCfg<bf16_t, 32> { static constexpr int T = 13, K = 2048, CPL = 8; };
+template <> struct TileCfg<bf16_t, 64> { static constexpr int T = 9, K = 2048, CPL = 8; };
 template <> struct TileCfg<__half, 16> : TileCfg<bf16_t, 16> {};
 template <> struct TileCfg<__half, 32> : TileCfg<bf16_t, 32> {};
 template <> struct TileCfg<__half, 64> : TileCfg<bf16_t, 64> {};
@@ -100,7 +100,8 @@ __host__ __device__ constexpr size_t tile_lds_bytes() {
          static_cast<size_t>(4 * NPOS) * C * 4 +           // corner planes
          static_cast<size_t>(K) * 16 +                     // sorted records
          static_cast<size_t>(3 * NPOS) * 4 +               // position count, offset, order
-         64 * 4 +                                          // count buckets
+         2 * 64 * 4 +                                      // count buckets, bucket starts
+         16 * 4 +                                          // per-wavefront count totals
          static_cast<size_t>(C) * 4;                       // zero slot
 }
 
@@ -464,17 +465,30 @@ __device__ __forceinline__ uint32_t item_batches(const Item &d) {
   return (d.r1 - d.r0 + K - 1) / K;
 }
 
+// Eight channels per lane: 32 bytes of fp32 (two 16-byte accesses) or 16
+// bytes of fp16/bf16 (works on LDS and global pointers).
+__device__ __forceinline__ void load8ch(const float *p, float (&o)[8]) {
+  const float4 a = reinterpret_cast<const float4 *>(p)[0];
+  const float4 b = reinterpret_cast<const float4 *>(p)[1];
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+__device__ __forceinline__ void load8ch(const bf16_t *p, float (&o)[8]) { load16(p, o); }
+__device__ __forceinline__ void load8ch(const __half *p, float (&o)[8]) { load16(p, o); }
+
 // One work item = records [r0, r1) of a tile of T x T value cells. The
 // records are processed in batches of K: counting-sorted by top-left corner
 // position ((T+1)^2 positions, [-1, T-1]^2 in the tile frame) in LDS; lane
-// group g then owns positions of rank g, g + NG, ... in decreasing-count
-// order and accumulates, in registers, the four corner sums
-// S_p[d] = sum_r w_d(r) * attn(r) * grad_out[q(r)] of each; S_p[d] is added
-// to slot p of corner plane d (no other group writes it). At the end of the
-// item, cell (r, c) sums slot (r - dy, c - dx) of plane (dy, dx). Per record
-// the owner group also computes the four corner dot products
-// D_d = grad_out . v_d from the LDS value tile, from which one thread per
-// record forms the attention and location gradients:
+// group g (KQ lanes of 8 channels) then owns positions of rank g,
+// 2 NG - 1 - g, 2 NG + g, ... (ranks in decreasing-count order) and
+// accumulates, in registers, the four corner sums
+// S_p[d] = sum_r w_d(r) * attn(r) * grad_out[q(r)] of each; S_p[d] goes to
+// slot p of corner plane d (no other group writes it): stored by the item's
+// first batch, which visits every position, added by its later batches. At
+// the end of the item, cell (r, c) sums slot (r - dy, c - dx) of plane
+// (dy, dx). Per record the owner group also computes the four corner dot
+// products D_d = grad_out . v_d from the LDS value tile, from which one
+// thread per record forms the attention and location gradients:
 //   grad_attn = sum_d w_d D_d,
 //   grad_ix = attn * (wy0 (D1 - D0) + wy1 (D3 - D2)),
 //   grad_iy = attn * (wx0 (D2 - D0) + wx1 (D3 - D1)),
@@ -482,18 +496,19 @@ __device__ __forceinline__ uint32_t item_batches(const Item &d) {
 // grid_sample's bilinear backward (zeros padding) regrouped by corner; they
 // are stored over the record's own (consumed) slot for msda_grad_gather.
 //
-// Memory order: gfx950 counts loads and stores in one in-order vmcnt, so the
-// owner loop (which loads grad_out rows one record ahead) waits for every
-// earlier memory operation. The next batch's records and value tile are
-// therefore issued first thing in a batch, and the stores of finished work
-// right after them, well before the owner phase.
+// Memory order: gfx950 counts loads and stores in one in-order vmcnt, so a
+// wait for one load also waits for everything issued before it. The next
+// batch's records are loaded first thing in a batch (into registers); the
+// next item's value tile is copied into LDS by buffer-to-LDS loads issued at
+// the end of the previous batch (no registers held), waited for before the
+// owner phase; the owner loop keeps NR grad_out rows in flight per group.
 template <typename VT, int C>
 __global__ void __launch_bounds__(kTileBlock)
-    msda_tile_backward(const VT *__restrict__ value, const int64_t *__restrict__ shapes,
-                       const int64_t *__restrict__ starts, const VT *__restrict__ grad_out,
-                       uint4 *__restrict__ records, const Item *__restrict__ items,
-                       const uint32_t *__restrict__ item_total, Shape s, BinPlan p,
-                       float *__restrict__ grad_value) {
+    msda_tile_backward(const VT *__restrict__ value, uint32_t value_bytes,
+                       const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
+                       const VT *__restrict__ grad_out, uint4 *__restrict__ records,
+                       const Item *__restrict__ items, const uint32_t *__restrict__ item_total,
+                       Shape s, BinPlan p, float *__restrict__ grad_value) {
   using Cfg = TileCfg<VT, C>;
   constexpr int T = Cfg::T, K = Cfg::K, CPL = Cfg::CPL;
   constexpr int TV = T + 1, NPOS = TV * TV;
@@ -503,7 +518,8 @@ __global__ void __launch_bounds__(kTileBlock)
   constexpr int UPV = C * VB / 16;     // 16-byte units per value row
   constexpr int VPT = (NPOS * UPV + kTileBlock - 1) / kTileBlock;  // value units per thread
   constexpr int RPT = K / kTileBlock;  // records per thread
-  static_assert(CPL == 4 && (KQ & (KQ - 1)) == 0 && KQ <= kWave, "bad lane layout");
+  constexpr int NR = 4;                // grad_out rows in flight per group
+  static_assert(CPL == 8 && (KQ & (KQ - 1)) == 0 && KQ >= 2 && KQ <= kWave, "bad lane layout");
   static_assert(K % kTileBlock == 0 && NPOS <= kTileBlock, "bad batch size");
   static_assert(tile_lds_bytes<VT, C>() + 3400 <= kTileLdsLimit, "tile LDS budget");
 
@@ -513,17 +529,21 @@ __global__ void __launch_bounds__(kTileBlock)
   VT *vt = reinterpret_cast<VT *>(lds);  // NPOS cells + one zero row
   float *planes = reinterpret_cast<float *>(lds + static_cast<size_t>(NPOS + 1) * C * VB);
   uint4 *stash = reinterpret_cast<uint4 *>(planes + 4 * NPOS * C);
-  uint32_t *pcount = reinterpret_cast<uint32_t *>(stash + K);
+  float *dummy = reinterpret_cast<float *>(stash + K);  // [C], always zero (16-byte aligned)
+  uint32_t *pcount = reinterpret_cast<uint32_t *>(dummy + C);
   uint32_t *poff = pcount + NPOS;
   uint32_t *order = poff + NPOS;
-  uint32_t *bucket = order + NPOS;                         // [64]
-  float *dummy = reinterpret_cast<float *>(bucket + 64);  // [C], always zero
+  uint32_t *bucket = order + NPOS;  // [64] positions per count bucket
+  uint32_t *bstart = bucket + 64;   // [64] first rank of each bucket
+  uint32_t *wsum = bstart + 64;     // [16] counts per wavefront of positions
 
   stage_levels(lv, shapes, starts, s);
   stage_tiles<T>(lv, s.levels, ntc, base);
   const int MC = s.heads * C;
   const int tid = threadIdx.x;
+  const int lane = tid % kWave, wave = tid / kWave;
   const int grp = tid / KQ, k = tid % KQ;
+  const __amdgpu_buffer_rsrc_t vrsrc = make_rsrc(value, value_bytes);
 
   // this workgroup's items: lo + wid, lo + wid + nw, ... below hi
   constexpr int kXcd = 8;
@@ -580,61 +600,72 @@ __global__ void __launch_bounds__(kTileBlock)
     const size_t at = c.valid && i < s1 ? rec_base(c.d) + i : 0;
     return records[at];
   };
-  auto geom = [&](const BatchCursor &c) { return item_geom(c.d); };
   auto slab_offset = [&](const Item &d) {
     return static_cast<size_t>(d.b) * s.spatial * MC + d.m * C;
   };
-  // source of 16-byte unit v of the value tile (cells [0, T]^2) of c's item;
-  // `ok` false for units past the tile or cells outside the level (stored as
-  // zeros)
-  auto value_unit_src = [&](const BatchCursor &c, int v, bool &ok) {
-    const TileGeom g = geom(c);
+  // Value tile (cells [0, T]^2 of the item's frame) of d into LDS with
+  // buffer-to-LDS loads: 16-byte unit u of the tile goes to vt + 16 u; each
+  // wavefront moves 64 consecutive units (lane i to M0 + 16 i), so the LDS
+  // base of a load is wavefront-uniform. Units of cells outside the level use
+  // an offset past the end of value and read zeros. value_bytes < 2^31 is
+  // checked on the host.
+  auto stage_value_tile = [&](const Item &d) {
+    const TileGeom g = item_geom(d);
     const Level L = lv[g.l];
-    const int unit = tid + v * kTileBlock;
-    const int u = unit < NPOS * UPV ? unit : 0;
-    const int cell = u / UPV, kk = u % UPV;
-    const int y = g.y_lo + cell / TV, x = g.x_lo + cell % TV;
-    ok = c.valid && unit < NPOS * UPV && y < L.h && x < L.w;
-    const size_t at =
-        ok ? slab_offset(c.d) + static_cast<size_t>(L.start + y * L.w + x) * MC : 0;
-    return reinterpret_cast<const uint4 *>(value + at) + (ok ? kk : 0);
-  };
-  auto store_value_units = [&](const uint4 (&u)[VPT], const bool (&ok)[VPT]) {
+    const size_t slab = slab_offset(d);
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
       const int unit = tid + v * kTileBlock;
       if (unit < NPOS * UPV) {
-        reinterpret_cast<uint4 *>(vt)[unit] = ok[v] ? u[v] : make_uint4(0u, 0u, 0u, 0u);
+        const int cell = unit / UPV, kk = unit % UPV;
+        const int y = g.y_lo + cell / TV, x = g.x_lo + cell % TV;
+        const uint32_t off =
+            y < L.h && x < L.w
+                ? static_cast<uint32_t>(
+                      (slab + static_cast<size_t>(L.start + y * L.w + x) * MC) * VB) +
+                      static_cast<uint32_t>(kk * 16)
+                : kOobOffset;
+        unsigned char *dst = reinterpret_cast<unsigned char *>(vt) +
+                             static_cast<size_t>(wave * kWave + v * kTileBlock) * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            vrsrc, (__attribute__((address_space(3))) void *)dst, 16, off, 0, 0, 0);
       }
     }
   };
-  // cell sums of a finished item's corner planes to grad_value; every plane
-  // slot that maps to a cell of [0, T]^2 is read once and zeroed (slots that
-  // map to row or column -1 only ever hold contributions of invalid corners)
+  // cell sums of a finished item's corner planes to grad_value (slots that
+  // map to row or column -1 only ever hold contributions of invalid corners
+  // and are not read); four channels per thread and step
   auto write_back = [&](const Item &d) {
+    constexpr int C4 = C / 4;
     const TileGeom g = item_geom(d);
     const Level Lw = lv[g.l];
     const bool split = (d.tile & kSplitBit) != 0;
     const size_t slab = slab_offset(d);
-    for (int i = tid; i < NPOS * C; i += kTileBlock) {
-      const int cell = i / C, ch = i % C;
+    for (int i = tid; i < NPOS * C4; i += kTileBlock) {
+      const int cell = i / C4, ch = (i % C4) * 4;
       const int r = cell / TV, c = cell % TV;  // cell (r, c) of [0, T]^2
-      float sum = 0.0f;
+      const int y = g.y_lo + r, x = g.x_lo + c;
+      if (y >= Lw.h || x >= Lw.w) continue;
+      float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int pr = r - (q >> 1), pc = c - (q & 1);  // position, >= -1
-        float *pl = pr < T && pc < T ? planes + (q * NPOS + (pr + 1) * TV + pc + 1) * C + ch
-                                     : dummy + ch;  // always zero
-        sum += *pl;
-        *pl = 0.0f;
+        const float4 v = *reinterpret_cast<const float4 *>(
+            pr < T && pc < T ? planes + (q * NPOS + (pr + 1) * TV + pc + 1) * C + ch
+                             : dummy + ch);  // always zero
+        sum.x += v.x;
+        sum.y += v.y;
+        sum.z += v.z;
+        sum.w += v.w;
       }
-      const int y = g.y_lo + r, x = g.x_lo + c;
-      if (y >= Lw.h || x >= Lw.w) continue;
       float *dst = grad_value + slab + static_cast<size_t>(Lw.start + y * Lw.w + x) * MC + ch;
       if (!split && r < T && c < T && !boundary_cell(r, c, g)) {
-        *dst = sum;
+        *reinterpret_cast<float4 *>(dst) = sum;
       } else {
-        unsafeAtomicAdd(dst, sum);
+        unsafeAtomicAdd(dst, sum.x);
+        unsafeAtomicAdd(dst + 1, sum.y);
+        unsafeAtomicAdd(dst + 2, sum.z);
+        unsafeAtomicAdd(dst + 3, sum.w);
       }
     }
   };
@@ -643,95 +674,83 @@ __global__ void __launch_bounds__(kTileBlock)
   uint4 r_cur[RPT];
 #pragma unroll
   for (int u = 0; u < RPT; ++u) r_cur[u] = load_record(c0, u);
-  {
-    uint4 u0[VPT];
-    bool ok0[VPT];
-#pragma unroll
-    for (int v = 0; v < VPT; ++v) u0[v] = *value_unit_src(c0, v, ok0[v]);
-    store_value_units(u0, ok0);
-  }
+  stage_value_tile(c0.d);
   if (tid < UPV) reinterpret_cast<uint4 *>(vt + NPOS * C)[tid] = make_uint4(0u, 0u, 0u, 0u);
   if (tid < C) dummy[tid] = 0.0f;
-  for (int i = tid; i < NPOS * C; i += kTileBlock) {
-    reinterpret_cast<float4 *>(planes)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  }
   if (tid < NPOS) pcount[tid] = 0;
+  if (tid < kWave) bucket[tid] = 0;
   __syncthreads();
 
-  // this thread's finished records of the previous batch: result and slot
-  int ns_prev = 0;
-  size_t f_base = 0;
-  uint32_t f_s0 = 0;
-  float f_ga[RPT], f_gx[RPT], f_gy[RPT];
-  const uint32_t smask = (1u << p.lp_log2) - 1u;
-  (void)smask;
   for (;;) {
-    const TileGeom g0 = geom(c0);
+    const TileGeom g0 = item_geom(c0.d);
     const Level L = lv[g0.l];
     uint32_t s0, s1;
     batch_range(c0, s0, s1);
     const int ns = static_cast<int>(s1 - s0);
+    const bool first_of_item = c0.k == 0;
     const bool last_of_item = c0.k + 1 == item_batches<K>(c0.d);
     const bool next_new_item = c1.valid && c1.k == 0;
     const int b0 = static_cast<int>(c0.d.b), m0 = static_cast<int>(c0.d.m);
 
-    // A. next batch's records and value tile first; then the previous
-    // batch's results; then this batch's sort keys
+    // A. next batch's records; this batch's sort keys. Record slots are
+    // u * kTileBlock + tid; a wavefront whose first slot is past the batch
+    // skips the per-record work.
     uint4 r_next[RPT];
 #pragma unroll
     for (int u = 0; u < RPT; ++u) r_next[u] = load_record(c1, u);
-    uint4 v_next[VPT];
-    bool v_ok[VPT];
-#pragma unroll
-    for (int v = 0; v < VPT; ++v) v_next[v] = *value_unit_src(c1, v, v_ok[v]);
-#pragma unroll
-    for (int u = 0; u < RPT; ++u) {
-      const int i = tid + u * kTileBlock;
-      if (i < ns_prev) {
-        records[f_base + f_s0 + i] = make_uint4(__float_as_uint(f_ga[u]), __float_as_uint(f_gx[u]),
-                                                __float_as_uint(f_gy[u]), 0u);
-      }
-    }
+    const int wave_slot = tid & ~(kWave - 1);
     int pos[RPT];
     uint32_t rank[RPT];
-    uint4 entry[RPT];
-    float my_wx1[RPT], my_wy1[RPT], my_a[RPT];
+    float my_wx1[RPT], my_wy1[RPT];
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
       const int i = tid + u * kTileBlock;
       pos[u] = -1;
       rank[u] = 0;
-      const Tap t = make_tap(__uint_as_float(r_cur[u].y), __uint_as_float(r_cur[u].z), L, i < ns);
-      const int py = t.y0 - g0.y_lo + 1, px = t.x0 - g0.x_lo + 1;
-      my_wx1[u] = t.wx1;
-      my_wy1[u] = t.wy1;
-      my_a[u] = __uint_as_float(r_cur[u].w);
-      entry[u] = make_uint4(r_cur[u].x, __float_as_uint(t.wx1), __float_as_uint(t.wy1), r_cur[u].w);
-      if (t.in && py >= 0 && py < TV && px >= 0 && px < TV) {  // always, for binned records
-        pos[u] = py * TV + px;
-        rank[u] = atomicAdd(&pcount[pos[u]], 1u);
+      my_wx1[u] = my_wy1[u] = 0.0f;
+      if (wave_slot + u * kTileBlock < ns) {
+        const Tap t =
+            make_tap(__uint_as_float(r_cur[u].y), __uint_as_float(r_cur[u].z), L, i < ns);
+        const int py = t.y0 - g0.y_lo + 1, px = t.x0 - g0.x_lo + 1;
+        my_wx1[u] = t.wx1;
+        my_wy1[u] = t.wy1;
+        if (t.in && py >= 0 && py < TV && px >= 0 && px < TV) {  // always, for binned records
+          pos[u] = py * TV + px;
+          rank[u] = atomicAdd(&pcount[pos[u]], 1u);
+        }
       }
     }
     __syncthreads();
 
-    // B. (one wavefront) exclusive scan of the position counts, then the
-    // positions in order of decreasing count (counting sort on min(n, 63))
-    if (tid < kWave) {
-      uint32_t carry = 0;
-      for (int c = 0; c < NPOS; c += kWave) {
-        const int i = c + tid;
-        const uint32_t v = i < NPOS ? pcount[i] : 0u;
-        uint32_t incl = v;
+    // B. positions in order of decreasing count (counting sort on
+    // min(n, 63)) and the exclusive scan of the counts, one thread per
+    // position: B1 scans within wavefronts and ranks each position in its
+    // count bucket, B2 adds the wavefront totals and scans the buckets, B3
+    // places each position.
+    constexpr int kPosWaves = (NPOS + kWave - 1) / kWave;
+    uint32_t p_cnt = 0, p_incl = 0, p_brank = 0;
+    int p_bk = 0;
+    if (tid < kPosWaves * kWave) {
+      p_cnt = tid < NPOS ? pcount[tid] : 0u;
+      p_incl = p_cnt;
 #pragma unroll
-        for (int d = 1; d < kWave; d <<= 1) {
-          const uint32_t up = __shfl_up(incl, d, kWave);
-          if (tid >= d) incl += up;
-        }
-        if (i < NPOS) poff[i] = carry + incl - v;
-        carry += __shfl(incl, kWave - 1, kWave);
+      for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t up = __shfl_up(p_incl, d, kWave);
+        if (lane >= d) p_incl += up;
       }
-      bucket[tid] = 0;
-      for (int i = tid; i < NPOS; i += kWave) atomicAdd(&bucket[63 - min(pcount[i], 63u)], 1u);
+      if (lane == kWave - 1) wsum[wave] = p_incl;
+      if (tid < NPOS) {
+        p_bk = 63 - static_cast<int>(min(p_cnt, 63u));
+        p_brank = atomicAdd(&bucket[p_bk], 1u);
+      }
+    }
+    __syncthreads();
+    if (tid < NPOS) {
+      uint32_t before = 0;
+      for (int w = 0; w < wave; ++w) before += wsum[w];
+      poff[tid] = before + p_incl - p_cnt;
+    }
+    if (tid < kWave) {
       const uint32_t v = bucket[tid];
       uint32_t incl = v;
 #pragma unroll
@@ -739,146 +758,163 @@ __global__ void __launch_bounds__(kTileBlock)
         const uint32_t up = __shfl_up(incl, d, kWave);
         if (tid >= d) incl += up;
       }
-      bucket[tid] = incl - v;
-      for (int i = tid; i < NPOS; i += kWave) {
-        order[atomicAdd(&bucket[63 - min(pcount[i], 63u)], 1u)] = static_cast<uint32_t>(i);
-      }
+      bstart[tid] = incl - v;
     }
     __syncthreads();
+    if (tid < NPOS) order[bstart[p_bk] + p_brank] = static_cast<uint32_t>(tid);
 
-    // C. records in position order
+    // C. records in position order; the value tile of a new item (copied by
+    // buffer-to-LDS loads issued in the previous batch) has landed once this
+    // thread's loads are done, and every thread's after the barrier
     uint32_t my_slot[RPT];
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
       my_slot[u] = 0;
-      if (pos[u] >= 0) {
+      if (wave_slot + u * kTileBlock < ns && pos[u] >= 0) {
         my_slot[u] = poff[pos[u]] + rank[u];
-        stash[my_slot[u]] = entry[u];
+        stash[my_slot[u]] = make_uint4(r_cur[u].x, __float_as_uint(my_wx1[u]),
+                                       __float_as_uint(my_wy1[u]), r_cur[u].w);
       }
     }
+    if (first_of_item) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) only
     __syncthreads();
 
-    // D. owners: lane group grp takes ranks grp, grp + NG, ...
+    // D. owners: lane group grp takes ranks grp, 2 NG - 1 - grp, 2 NG + grp, ...
+    // (snake order: the owners of the largest positions of one round get the
+    // smallest of the next). The first batch of an item visits every position
+    // (zero-count ones store zero sums); later batches stop at the first empty
+    // position and add.
     const VT *gbase =
         grad_out + (static_cast<size_t>(b0) * s.queries * s.heads + m0) * C + k * CPL;
     const uint32_t q_stride = static_cast<uint32_t>(s.heads * C);  // grad_out row stride
+    const u32x4 *vstash = reinterpret_cast<const u32x4 *>(stash);
+    float *stash_f = reinterpret_cast<float *>(stash);
+    // q < 2^24 and q * q_stride < 2^32 (checked on the host): a 24-bit multiply
+    auto grow = [&](uint32_t id) {
+      const uint32_t q = min(id >> p.lp_log2, static_cast<uint32_t>(s.queries - 1));
+      return gbase + __umul24(q, q_stride);
+    };
 #pragma unroll 1
-    for (int i = grp; i < NPOS; i += NG) {
+    for (int rnd = 0; rnd * NG < NPOS; ++rnd) {
+      const int i = rnd * NG + ((rnd & 1) ? NG - 1 - grp : grp);
+      if (i >= NPOS) break;  // later rounds start further out
       const int p_id = static_cast<int>(order[i]);
       const uint32_t n = pcount[p_id];
-      if (n == 0) break;  // positions are in order of decreasing count
-      const uint32_t first = poff[p_id];
-      const int py = p_id / TV - 1, px = p_id % TV - 1;  // tile frame, >= -1
-      // corner value rows (row -1 or column -1: the zero row after the tile)
-      float v[4][CPL];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int cy = py + (d >> 1), cx = px + (d & 1);
-        load4ch(vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * C : NPOS * C) + k * CPL, v[d]);
-      }
+      if (n == 0 && !first_of_item) break;  // positions are in order of decreasing count
       float acc[4][CPL];
 #pragma unroll
       for (int d = 0; d < 4; ++d)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) acc[d][j] = 0.0f;
-      // records in two register sets A and B, each refilled as soon as it is
-      // consumed: every wait for a grad_out row leaves the other in flight
-      auto grow = [&](uint32_t id) {
-        const uint32_t q = min(id >> p.lp_log2, static_cast<uint32_t>(s.queries - 1));
-        return gbase + static_cast<uint32_t>(q * q_stride);
-      };
-      auto one_record = [&](const u32x4 &e, const float (&gv)[CPL], uint32_t slot) {
-        const float wx1 = __uint_as_float(e.y), wy1 = __uint_as_float(e.z);
-        const float a = __uint_as_float(e.w);
-        const float ay0 = (1.0f - wy1) * a, ay1 = wy1 * a;
-        const float wx0 = 1.0f - wx1;
-        const float wa[4] = {ay0 * wx0, ay0 * wx1, ay1 * wx0, ay1 * wx1};
-        float D[4];
+      if (n > 0) {
+        const uint32_t first = poff[p_id];
+        const int py = p_id / TV - 1, px = p_id % TV - 1;  // tile frame, >= -1
+        // corner value rows (row -1 or column -1: the zero row after the tile)
+        float v[4][CPL];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          float dd = 0.0f;
+          const int cy = py + (d >> 1), cx = px + (d & 1);
+          load8ch(vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * C : NPOS * C) + k * CPL, v[d]);
+        }
+        auto one_record = [&](const u32x4 &e, const float (&gv)[CPL], uint32_t slot) {
+          const float wx1 = __uint_as_float(e.y), wy1 = __uint_as_float(e.z);
+          const float a = __uint_as_float(e.w);
+          const float ay0 = (1.0f - wy1) * a, ay1 = wy1 * a;
+          const float wx0 = 1.0f - wx1;
+          const float wa[4] = {ay0 * wx0, ay0 * wx1, ay1 * wx0, ay1 * wx1};
+          float D[4];
 #pragma unroll
-          for (int j = 0; j < CPL; ++j) {
-            acc[d][j] += wa[d] * gv[j];
-            dd += gv[j] * v[d][j];
+          for (int d = 0; d < 4; ++d) {
+            float dd = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+              acc[d][j] += wa[d] * gv[j];
+              dd += gv[j] * v[d][j];
+            }
+            D[d] = group_sum<KQ>(dd);
           }
-          D[d] = group_sum<KQ>(dd);
+          // D_0..D_3 replace the consumed record (read by this group alone):
+          // lane k < 4 stores D_k (KQ >= 4), lane k stores D_2k, D_2k+1 (KQ 2)
+          if constexpr (KQ >= 4) {
+            const float dk = k == 0 ? D[0] : k == 1 ? D[1] : k == 2 ? D[2] : D[3];
+            if (KQ == 4 || k < 4) stash_f[slot * 4 + k] = dk;
+          } else {
+            reinterpret_cast<float2 *>(stash_f)[slot * 2 + k] =
+                k == 0 ? make_float2(D[0], D[1]) : make_float2(D[2], D[3]);
+          }
+        };
+        // NR records in flight: register set j holds record r + j and is
+        // refilled with record r + j + NR as soon as it is consumed. Past the
+        // end of the list a set keeps its (consumed) record: a processed slot
+        // holds D values, not a record id.
+        u32x4 e[NR];
+        float g[NR][CPL];
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+          e[j] = vstash[first + min(static_cast<uint32_t>(j), n - 1)];
+          load8ch(grow(e[j].x), g[j]);
         }
-        // D_0..D_3 replace the consumed record (read by this group alone)
-        if (k == 0) {
-          stash[slot] = make_uint4(__float_as_uint(D[0]), __float_as_uint(D[1]),
-                                   __float_as_uint(D[2]), __float_as_uint(D[3]));
+        for (uint32_t r = 0; r < n; r += NR) {
+#pragma unroll
+          for (int j = 0; j < NR; ++j) {
+            if (r + j < n) one_record(e[j], g[j], first + r + j);
+            const uint32_t nx = r + j + NR;
+            const u32x4 t = vstash[first + min(nx, n - 1)];
+            e[j] = nx < n ? t : e[j];
+            load8ch(grow(e[j].x), g[j]);
+          }
         }
-      };
-      // native vector registers (HIP's uint4 under a select lands in scratch)
-      const u32x4 *vstash = reinterpret_cast<const u32x4 *>(stash);
-      u32x4 eA = vstash[first], eB = vstash[first + min(1u, n - 1)];
-      float gA[CPL], gB[CPL];
-      load4ch(grow(eA.x), gA);
-      load4ch(grow(eB.x), gB);
-      // Past the end of the list a set keeps its (consumed) record: a slot
-      // already processed holds D values, not a record id.
-      for (uint32_t r = 0; r < n; r += 2) {
-        one_record(eA, gA, first + r);
-        const u32x4 tA = vstash[first + min(r + 2, n - 1)];
-        eA = r + 2 < n ? tA : eA;
-        load4ch(grow(eA.x), gA);
-        if (r + 1 < n) one_record(eB, gB, first + r + 1);
-        const u32x4 tB = vstash[first + min(r + 3, n - 1)];
-        eB = r + 3 < n ? tB : eB;
-        load4ch(grow(eB.x), gB);
       }
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         float4 *dst = reinterpret_cast<float4 *>(planes + (d * NPOS + p_id) * C + k * CPL);
-        float4 cur = *dst;
-        cur.x += acc[d][0];
-        cur.y += acc[d][1];
-        cur.z += acc[d][2];
-        cur.w += acc[d][3];
-        *dst = cur;
+#pragma unroll
+        for (int h = 0; h < CPL / 4; ++h) {
+          float4 cur = make_float4(acc[d][4 * h], acc[d][4 * h + 1], acc[d][4 * h + 2],
+                                   acc[d][4 * h + 3]);
+          if (!first_of_item) {
+            const float4 old = dst[h];
+            cur.x += old.x;
+            cur.y += old.y;
+            cur.z += old.z;
+            cur.w += old.w;
+          }
+          dst[h] = cur;
+        }
       }
     }
     __syncthreads();
 
-    // E. this batch's location/weight gradients (stored during the next
-    // batch), position counts reset, a finished item written back, the next
-    // value tile staged
+    // E. this batch's location/weight gradients over the records' slots,
+    // position counts reset, a finished item written back, the next item's
+    // value tile requested
+    const size_t rb = rec_base(c0.d) + s0;
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
       const int i = tid + u * kTileBlock;
-      f_ga[u] = f_gx[u] = f_gy[u] = 0.0f;
-      if (i < ns) {
+      if (wave_slot + u * kTileBlock < ns && i < ns) {
         const uint4 Dr = stash[my_slot[u]];
         const float D0 = __uint_as_float(Dr.x), D1 = __uint_as_float(Dr.y);
         const float D2 = __uint_as_float(Dr.z), D3 = __uint_as_float(Dr.w);
-        const float wx1 = my_wx1[u], wy1 = my_wy1[u], a = my_a[u];
+        const float wx1 = my_wx1[u], wy1 = my_wy1[u], a = __uint_as_float(r_cur[u].w);
         const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
-        f_ga[u] = wy0 * (wx0 * D0 + wx1 * D1) + wy1 * (wx0 * D2 + wx1 * D3);
-        f_gx[u] = a * (wy0 * (D1 - D0) + wy1 * (D3 - D2)) * L.fw;
-        f_gy[u] = a * (wx0 * (D2 - D0) + wx1 * (D3 - D1)) * L.fh;
+        const float ga = wy0 * (wx0 * D0 + wx1 * D1) + wy1 * (wx0 * D2 + wx1 * D3);
+        const float gx = a * (wy0 * (D1 - D0) + wy1 * (D3 - D2)) * L.fw;
+        const float gy = a * (wx0 * (D2 - D0) + wx1 * (D3 - D1)) * L.fh;
+        records[rb + i] =
+            make_uint4(__float_as_uint(ga), __float_as_uint(gx), __float_as_uint(gy), 0u);
       }
     }
-    ns_prev = ns;
-    f_base = rec_base(c0.d);
-    f_s0 = s0;
     if (tid < NPOS) pcount[tid] = 0;
+    if (tid < kWave) bucket[tid] = 0;
     if (last_of_item) write_back(c0.d);
-    if (next_new_item) store_value_units(v_next, v_ok);
+    if (next_new_item) stage_value_tile(c1.d);
 #pragma unroll
     for (int u = 0; u < RPT; ++u) r_cur[u] = r_next[u];
     c0 = c1;
     c1 = advance(c1);
     __syncthreads();
     if (!c0.valid) break;
-  }
-#pragma unroll
-  for (int u = 0; u < RPT; ++u) {
-    const int i = tid + u * kTileBlock;
-    if (i < ns_prev) {
-      records[f_base + f_s0 + i] = make_uint4(__float_as_uint(f_ga[u]), __float_as_uint(f_gx[u]),
-                                              __float_as_uint(f_gy[u]), 0u);
-    }
   }
 }
 

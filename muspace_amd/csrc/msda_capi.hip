@@ -367,6 +367,13 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   p.tile_bound = static_cast<int>(bound);
   p.lp_log2 = log2_int(s.lp > 0 ? s.lp : 1);
   if ((static_cast<int64_t>(s.queries) << p.lp_log2) > (int64_t{1} << 32)) return false;
+  // the tile kernel addresses grad_out rows with a 24-bit multiply (q < 2^24)
+  // and a 32-bit element offset inside one batch entry
+  if (s.queries >= (1 << 24)) return false;
+  // the tile kernel stages value tiles with 32-bit buffer offsets below kOobOffset
+  const size_t vb = value_dtype == MUSPACE_DTYPE_F32 ? 4 : 2;
+  if (value_bytes(s, vb) + 64 > msda::kOobOffset) return false;
+  if (static_cast<int64_t>(s.queries) * s.heads * s.channels >= (int64_t{1} << 32)) return false;
   p.rec_cap = static_cast<int64_t>(s.queries) * s.lp;
   if (p.rec_cap >= (int64_t{1} << 31)) return false;
   const int64_t bm = static_cast<int64_t>(s.batch) * s.heads;
@@ -436,7 +443,8 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
       shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
   scatter<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(
       shapes, starts, lc, aw, s, p, counts, zero_tiles, records, rec_of_sample, gv);
-  tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, shapes, starts, go, records, items,
+  const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
+  tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, vbytes, shapes, starts, go, records, items,
                                                           item_total, s, p, gv);
   const int per_slab = static_cast<int>((p.rec_cap + msda::kBinBlock - 1) / msda::kBinBlock);
   msda::msda_grad_gather<<<bm * per_slab, msda::kBinBlock, 0, st>>>(rec_of_sample, records, s, p,
