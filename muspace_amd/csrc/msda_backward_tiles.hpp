@@ -476,6 +476,35 @@ __device__ __forceinline__ void load8ch(const float *p, float (&o)[8]) {
 __device__ __forceinline__ void load8ch(const bf16_t *p, float (&o)[8]) { load16(p, o); }
 __device__ __forceinline__ void load8ch(const __half *p, float (&o)[8]) { load16(p, o); }
 
+// The four corner dot products of one record, D_d = sum over the group's KQ
+// lanes of dd[d], by a reduce-scatter across the group (each step halves the
+// values a lane carries), stored to the record's slot d4[0..3]. KQ = 4: lane k
+// ends with D_k; KQ = 2: lane k with D_k and D_k+2; KQ = 8: lanes 4 + k of
+// the group with D_k (row_ror by 4 brings the other quad's sums).
+template <int KQ>
+__device__ __forceinline__ void store_corner_dots(const float (&dd)[4], int k, float *d4) {
+  const bool b0 = (k & 1) != 0;
+  // lanes k and k ^ 1: an even lane keeps corners 0 and 2, an odd lane 1 and 3
+  const float s0 = b0 ? dd[0] : dd[1], s1 = b0 ? dd[2] : dd[3];
+  const float k0 = (b0 ? dd[1] : dd[0]) + MSDA_DPP(s0, 0xB1);
+  const float k1 = (b0 ? dd[3] : dd[2]) + MSDA_DPP(s1, 0xB1);
+  if constexpr (KQ == 2) {
+    d4[k] = k0;
+    d4[k + 2] = k1;
+  } else {
+    // lanes k and k ^ 2: lanes 0, 1 keep corners 0, 1; lanes 2, 3 keep 2, 3
+    const bool b1 = (k & 2) != 0;
+    const float s = b1 ? k0 : k1;
+    float kk = (b1 ? k1 : k0) + MSDA_DPP(s, 0x4E);
+    if constexpr (KQ == 4) {
+      d4[k] = kk;
+    } else {
+      kk += MSDA_DPP(kk, 0x124);  // row_ror:4 -> lane i gets lane i - 4 of its row
+      if (k >= 4) d4[k - 4] = kk;
+    }
+  }
+}
+
 // One work item = records [r0, r1) of a tile of T x T value cells. The
 // records are processed in batches of K: counting-sorted by top-left corner
 // position ((T+1)^2 positions, [-1, T-1]^2 in the tile frame) in LDS; lane
@@ -519,7 +548,7 @@ __global__ void __launch_bounds__(kTileBlock)
   constexpr int VPT = (NPOS * UPV + kTileBlock - 1) / kTileBlock;  // value units per thread
   constexpr int RPT = K / kTileBlock;  // records per thread
   constexpr int NR = 4;                // grad_out rows in flight per group
-  static_assert(CPL == 8 && (KQ & (KQ - 1)) == 0 && KQ >= 2 && KQ <= kWave, "bad lane layout");
+  static_assert(CPL == 8 && (KQ == 2 || KQ == 4 || KQ == 8), "bad lane layout");
   static_assert(K % kTileBlock == 0 && NPOS <= kTileBlock, "bad batch size");
   static_assert(tile_lds_bytes<VT, C>() + 3400 <= kTileLdsLimit, "tile LDS budget");
 
@@ -701,13 +730,14 @@ __global__ void __launch_bounds__(kTileBlock)
     const int wave_slot = tid & ~(kWave - 1);
     int pos[RPT];
     uint32_t rank[RPT];
-    float my_wx1[RPT], my_wy1[RPT];
+    float my_wx1[RPT], my_wy1[RPT], my_a[RPT];
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
       const int i = tid + u * kTileBlock;
       pos[u] = -1;
       rank[u] = 0;
       my_wx1[u] = my_wy1[u] = 0.0f;
+      my_a[u] = __uint_as_float(r_cur[u].w);
       if (wave_slot + u * kTileBlock < ns) {
         const Tap t =
             make_tap(__uint_as_float(r_cur[u].y), __uint_as_float(r_cur[u].z), L, i < ns);
@@ -794,6 +824,13 @@ __global__ void __launch_bounds__(kTileBlock)
       const uint32_t q = min(id >> p.lp_log2, static_cast<uint32_t>(s.queries - 1));
       return gbase + __umul24(q, q_stride);
     };
+    // Round 0 hands the largest positions to the lowest wavefronts; they get
+    // issue priority over the wavefronts they share a SIMD with.
+    if (wave < kTileBlock / kWave / 2) {
+      __builtin_amdgcn_s_setprio(2);
+    } else {
+      __builtin_amdgcn_s_setprio(1);
+    }
 #pragma unroll 1
     for (int rnd = 0; rnd * NG < NPOS; ++rnd) {
       const int i = rnd * NG + ((rnd & 1) ? NG - 1 - grp : grp);
@@ -822,26 +859,18 @@ __global__ void __launch_bounds__(kTileBlock)
           const float ay0 = (1.0f - wy1) * a, ay1 = wy1 * a;
           const float wx0 = 1.0f - wx1;
           const float wa[4] = {ay0 * wx0, ay0 * wx1, ay1 * wx0, ay1 * wx1};
-          float D[4];
+          float dd[4];
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
-            float dd = 0.0f;
+            dd[d] = 0.0f;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
               acc[d][j] += wa[d] * gv[j];
-              dd += gv[j] * v[d][j];
+              dd[d] += gv[j] * v[d][j];
             }
-            D[d] = group_sum<KQ>(dd);
           }
-          // D_0..D_3 replace the consumed record (read by this group alone):
-          // lane k < 4 stores D_k (KQ >= 4), lane k stores D_2k, D_2k+1 (KQ 2)
-          if constexpr (KQ >= 4) {
-            const float dk = k == 0 ? D[0] : k == 1 ? D[1] : k == 2 ? D[2] : D[3];
-            if (KQ == 4 || k < 4) stash_f[slot * 4 + k] = dk;
-          } else {
-            reinterpret_cast<float2 *>(stash_f)[slot * 2 + k] =
-                k == 0 ? make_float2(D[0], D[1]) : make_float2(D[2], D[3]);
-          }
+          // D_0..D_3 replace the consumed record (read by this group alone)
+          store_corner_dots<KQ>(dd, k, stash_f + slot * 4);
         };
         // NR records in flight: register set j holds record r + j and is
         // refilled with record r + j + NR as soon as it is consumed. Past the
@@ -883,11 +912,19 @@ __global__ void __launch_bounds__(kTileBlock)
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();
 
-    // E. this batch's location/weight gradients over the records' slots,
-    // position counts reset, a finished item written back, the next item's
-    // value tile requested
+    // E. the next batch's records move into place first (the empty asm
+    // pins the wait for their loads here, before this phase's stores and
+    // buffer-to-LDS loads are issued); then this batch's location/weight
+    // gradients over the records' slots, position counts reset, a finished
+    // item written back, the next item's value tile requested
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+      r_cur[u] = r_next[u];
+      asm volatile("" : "+v"(r_cur[u].x), "+v"(r_cur[u].y), "+v"(r_cur[u].z), "+v"(r_cur[u].w));
+    }
     const size_t rb = rec_base(c0.d) + s0;
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
@@ -896,7 +933,7 @@ __global__ void __launch_bounds__(kTileBlock)
         const uint4 Dr = stash[my_slot[u]];
         const float D0 = __uint_as_float(Dr.x), D1 = __uint_as_float(Dr.y);
         const float D2 = __uint_as_float(Dr.z), D3 = __uint_as_float(Dr.w);
-        const float wx1 = my_wx1[u], wy1 = my_wy1[u], a = __uint_as_float(r_cur[u].w);
+        const float wx1 = my_wx1[u], wy1 = my_wy1[u], a = my_a[u];
         const float wx0 = 1.0f - wx1, wy0 = 1.0f - wy1;
         const float ga = wy0 * (wx0 * D0 + wx1 * D1) + wy1 * (wx0 * D2 + wx1 * D3);
         const float gx = a * (wy0 * (D1 - D0) + wy1 * (D3 - D2)) * L.fw;
@@ -909,8 +946,6 @@ __global__ void __launch_bounds__(kTileBlock)
     if (tid < kWave) bucket[tid] = 0;
     if (last_of_item) write_back(c0.d);
     if (next_new_item) stage_value_tile(c1.d);
-#pragma unroll
-    for (int u = 0; u < RPT; ++u) r_cur[u] = r_next[u];
     c0 = c1;
     c1 = advance(c1);
     __syncthreads();
