@@ -371,6 +371,22 @@ __global__ void __launch_bounds__(kBinBlock)
 
 // ---------------------------------------------------------- 3. scatter ---
 
+// Samples per sub-chunk of bin_scatter (a power of two; the chunk's queries
+// are processed kScatterSlots >> lp_log2 at a time).
+constexpr int kScatterSlots = 2048;
+constexpr int kScatterPerThread = kScatterSlots / kBinBlock;
+
+__host__ __device__ constexpr size_t scatter_lds_bytes(int tile_bound) {
+  return static_cast<size_t>(kScatterSlots) * 16 +       // records in arrival order
+         static_cast<size_t>(kScatterSlots) * 4 +        // tile-sorted slot list
+         static_cast<size_t>(2 * (tile_bound + 1)) * 4;  // write cursors, local offsets
+}
+
+// Writes each sample's 16-byte record into its tile's range and its record
+// index into the sample -> record map. A sub-chunk's records are first
+// ranked per tile and staged in LDS in arrival order, then written out in
+// tile order, so consecutive threads store consecutive records of one
+// tile's run (whole lines instead of one scattered 16-byte piece per lane).
 template <typename GT, int C, int T>
 __global__ void __launch_bounds__(kBinBlock)
     msda_bin_scatter(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
@@ -380,13 +396,17 @@ __global__ void __launch_bounds__(kBinBlock)
                      float *__restrict__ grad_value) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
-  extern __shared__ uint32_t cursor[];
+  __shared__ uint32_t part[kBinBlock / kWave];
+  extern __shared__ __align__(16) unsigned char dyn[];
+  uint4 *stage = reinterpret_cast<uint4 *>(dyn);                       // [kScatterSlots]
+  uint32_t *sorted = reinterpret_cast<uint32_t *>(stage + kScatterSlots);  // [kScatterSlots]
+  uint32_t *cursor = sorted + kScatterSlots;                         // [tile_bound + 1]
+  uint32_t *loff = cursor + (p.tile_bound + 1);                      // [tile_bound + 1]
   stage_levels(lv, shapes, starts, s);
   stage_tiles<T>(lv, s.levels, ntc, base);
   const int nt = base[s.levels];
   const uint32_t *row = counts + static_cast<size_t>(blockIdx.x) * p.tile_bound;
   for (int i = threadIdx.x; i < nt; i += blockDim.x) cursor[i] = row[i];
-  __syncthreads();
 
   const int bm = blockIdx.x / p.chunks, ch = blockIdx.x % p.chunks;
   const int b = bm / s.heads, m = bm % s.heads;
@@ -394,46 +414,86 @@ __global__ void __launch_bounds__(kBinBlock)
   const int nq = min(p.chunk_q, s.queries - q0);
   uint4 *rec = records + static_cast<size_t>(bm) * p.rec_cap;
   const int lpp = 1 << p.lp_log2;
-  const int total = nq * lpp;
-  // U samples per thread in flight: loads first (unconditional, clamped
-  // index), then the cursor atomics, then the stores
-  constexpr int U = 4;
-  for (int i0 = threadIdx.x; i0 < total; i0 += kBinBlock * U) {
-    float lx[U], ly[U], aw[U];
-    size_t o[U];
-    bool live[U];
-    int smp[U], q[U];
+  const int sub_q = kScatterSlots >> p.lp_log2;  // >= 1 (lpp <= kScatterSlots, checked on the host)
+  // each thread owns a contiguous run of tiles in the scans below
+  const int per = (nt + kBinBlock - 1) / kBinBlock;
+  const int t0 = min(nt, static_cast<int>(threadIdx.x) * per), t1 = min(nt, t0 + per);
+
+  for (int qs = 0; qs < nq; qs += sub_q) {
+    const int nsq = min(sub_q, nq - qs);
+    for (int i = threadIdx.x; i < nt; i += blockDim.x) loff[i] = 0;
+    __syncthreads();
+    // 1. loads first (every one unconditional, clamped index), then the tap,
+    // the rank inside its tile (LDS counter) and the record in arrival order
+    float lx[kScatterPerThread], ly[kScatterPerThread], aw[kScatterPerThread];
+    uint32_t key[kScatterPerThread];  // tile << 12 | slot, or kNoRecord
+    uint32_t rk[kScatterPerThread];   // rank inside the tile
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + u * kBinBlock;
-      q[u] = q0 + (i >> p.lp_log2);
-      smp[u] = i & (lpp - 1);
-      live[u] = i < total && smp[u] < s.lp;
-      o[u] = live[u] ? (static_cast<size_t>(b * s.queries + q[u]) * s.heads + m) * s.lp + smp[u]
-                     : 0;
-      lx[u] = to_float(loc[2 * o[u]]);
-      ly[u] = to_float(loc[2 * o[u] + 1]);
-      aw[u] = to_float(attn[o[u]]);
-    }
-    uint32_t at[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int l = level_of_sample(live[u] ? smp[u] : 0, s);
-      const Tap t = make_tap(lx[u], ly[u], lv[l], live[u]);
-      at[u] = kNoRecord;
-      if (t.in) at[u] = atomicAdd(&cursor[primary_tile<T>(t, ntc[l], base[l])], 1u);
+    for (int u = 0; u < kScatterPerThread; ++u) {
+      const int j = threadIdx.x + u * kBinBlock;  // slot: query j >> lp_log2, sample j & (lpp - 1)
+      const int q = q0 + qs + (j >> p.lp_log2), smp = j & (lpp - 1);
+      const bool live = (j >> p.lp_log2) < nsq && smp < s.lp;
+      const size_t o =
+          live ? (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp : 0;
+      lx[u] = to_float(loc[2 * o]);
+      ly[u] = to_float(loc[2 * o + 1]);
+      aw[u] = to_float(attn[o]);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (!live[u]) continue;
-      if (at[u] != kNoRecord) {
-        const uint32_t id =
-            (static_cast<uint32_t>(q[u]) << p.lp_log2) | static_cast<uint32_t>(smp[u]);
-        rec[at[u]] = make_uint4(id, __float_as_uint(lx[u]), __float_as_uint(ly[u]),
-                                __float_as_uint(aw[u]));
+    for (int u = 0; u < kScatterPerThread; ++u) {
+      const int j = threadIdx.x + u * kBinBlock;
+      const int q = q0 + qs + (j >> p.lp_log2), smp = j & (lpp - 1);
+      const bool live = (j >> p.lp_log2) < nsq && smp < s.lp;
+      const int l = level_of_sample(live ? smp : 0, s);
+      const Tap t = make_tap(lx[u], ly[u], lv[l], live);
+      key[u] = kNoRecord;
+      rk[u] = 0;
+      uint32_t at = kNoRecord;
+      if (t.in) {
+        const int tile = primary_tile<T>(t, ntc[l], base[l]);
+        const uint32_t rank = atomicAdd(&loff[tile], 1u);
+        key[u] = (static_cast<uint32_t>(tile) << 12) | static_cast<uint32_t>(j);
+        at = cursor[tile] + rank;
+        stage[j] = make_uint4((static_cast<uint32_t>(q) << p.lp_log2) | static_cast<uint32_t>(smp),
+                              __float_as_uint(lx[u]), __float_as_uint(ly[u]),
+                              __float_as_uint(aw[u]));
+        rk[u] = rank;
       }
-      rec_of_sample[o[u]] = at[u];
+      if (live) {
+        rec_of_sample[(static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp] = at;
+      }
     }
+    __syncthreads();
+    // 2. tile counts -> exclusive offsets (in place); the counts are kept as
+    // differences of consecutive offsets (loff[nt] = the sub-chunk's total)
+    uint32_t run = 0;
+    for (int t = t0; t < t1; ++t) run += loff[t];
+    uint32_t total;
+    uint32_t off = block_exclusive(run, part, &total);
+    for (int t = t0; t < t1; ++t) {
+      const uint32_t n = loff[t];
+      loff[t] = off;
+      off += n;
+    }
+    if (threadIdx.x == 0) loff[nt] = total;
+    __syncthreads();
+    // 3. tile-sorted list of slots
+#pragma unroll
+    for (int u = 0; u < kScatterPerThread; ++u) {
+      if (key[u] != kNoRecord) sorted[loff[key[u] >> 12] + rk[u]] = key[u];
+    }
+    __syncthreads();
+    // 4. records out in tile order: consecutive i of one tile are consecutive
+    // records of its global range
+    for (int i = threadIdx.x; i < static_cast<int>(total); i += kBinBlock) {
+      const uint32_t e = sorted[i];
+      const uint32_t tile = e >> 12, j = e & 0xfffu;
+      rec[cursor[tile] + (static_cast<uint32_t>(i) - loff[tile])] = stage[j];
+    }
+    __syncthreads();
+    // 5. cursors past this sub-chunk's records
+    for (int t = threadIdx.x; t < nt; t += blockDim.x) cursor[t] += loff[t + 1] - loff[t];
+    __syncthreads();
   }
 
   // non-boundary cells of the slab's empty and split tiles listed by

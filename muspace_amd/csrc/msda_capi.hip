@@ -365,7 +365,10 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   const int64_t bound = static_cast<int64_t>(s.spatial) / T + s.levels + 1;
   if (bound > msda::kMaxTilesPerSlab) return false;
   p.tile_bound = static_cast<int>(bound);
+  // bin_scatter stages a sub-chunk of records and two tile arrays in LDS
+  if (msda::scatter_lds_bytes(p.tile_bound) + 4096 > msda::kTileLdsLimit) return false;
   p.lp_log2 = log2_int(s.lp > 0 ? s.lp : 1);
+  if ((1 << p.lp_log2) > msda::kScatterSlots) return false;
   if ((static_cast<int64_t>(s.queries) << p.lp_log2) > (int64_t{1} << 32)) return false;
   // the tile kernel addresses grad_out rows with a 24-bit multiply (q < 2^24)
   // and a 32-bit element offset inside one batch entry
@@ -432,8 +435,9 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   constexpr size_t tile_bytes = msda::tile_lds_bytes<VT, C>();
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(count),
                             hipFuncAttributeMaxDynamicSharedMemorySize, hist_bytes);
+  const size_t scatter_bytes = msda::scatter_lds_bytes(p.tile_bound);
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(scatter),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, hist_bytes);
+                            hipFuncAttributeMaxDynamicSharedMemorySize, scatter_bytes);
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(tile),
                             hipFuncAttributeMaxDynamicSharedMemorySize, tile_bytes);
 
@@ -441,7 +445,7 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
                                                              item_total, gv);
   msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
       shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
-  scatter<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(
+  scatter<<<bm * p.chunks, msda::kBinBlock, scatter_bytes, st>>>(
       shapes, starts, lc, aw, s, p, counts, zero_tiles, records, rec_of_sample, gv);
   const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
   tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, vbytes, shapes, starts, go, records, items,
