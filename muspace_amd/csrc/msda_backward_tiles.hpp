@@ -172,7 +172,8 @@ __device__ __forceinline__ void zero_tile_cells(float *grad_value, size_t slab, 
 }
 
 // Block-wide exclusive scan of per-thread run totals (kBinBlock threads);
-// returns this thread's offset, writes the grand total to *total.
+// returns this thread's offset, writes the grand total to *total. Only LDS
+// is exchanged, so the barriers leave global memory operations in flight.
 __device__ __forceinline__ uint32_t block_exclusive(uint32_t run, uint32_t *part, uint32_t *total) {
   const int lane = threadIdx.x % kWave, wid = threadIdx.x / kWave;
   uint32_t incl = run;
@@ -182,14 +183,14 @@ __device__ __forceinline__ uint32_t block_exclusive(uint32_t run, uint32_t *part
     if (lane >= d) incl += up;
   }
   if (lane == kWave - 1) part[wid] = incl;
-  __syncthreads();
+  lds_barrier();
   uint32_t before = 0, all = 0;
   for (int w = 0; w < kBinBlock / kWave; ++w) {
     const uint32_t v = part[w];
     before += w < wid ? v : 0u;
     all += v;
   }
-  __syncthreads();
+  lds_barrier();
   *total = all;
   return before + incl - run;
 }
@@ -422,7 +423,7 @@ __global__ void __launch_bounds__(kBinBlock)
   for (int qs = 0; qs < nq; qs += sub_q) {
     const int nsq = min(sub_q, nq - qs);
     for (int i = threadIdx.x; i < nt; i += blockDim.x) loff[i] = 0;
-    __syncthreads();
+    lds_barrier();
     // 1. loads first (every one unconditional, clamped index), then the tap,
     // the rank inside its tile (LDS counter) and the record in arrival order
     float lx[kScatterPerThread], ly[kScatterPerThread], aw[kScatterPerThread];
@@ -463,7 +464,7 @@ __global__ void __launch_bounds__(kBinBlock)
         rec_of_sample[(static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp] = at;
       }
     }
-    __syncthreads();
+    lds_barrier();
     // 2. tile counts -> exclusive offsets (in place); the counts are kept as
     // differences of consecutive offsets (loff[nt] = the sub-chunk's total)
     uint32_t run = 0;
@@ -476,13 +477,13 @@ __global__ void __launch_bounds__(kBinBlock)
       off += n;
     }
     if (threadIdx.x == 0) loff[nt] = total;
-    __syncthreads();
+    lds_barrier();
     // 3. tile-sorted list of slots
 #pragma unroll
     for (int u = 0; u < kScatterPerThread; ++u) {
       if (key[u] != kNoRecord) sorted[loff[key[u] >> 12] + rk[u]] = key[u];
     }
-    __syncthreads();
+    lds_barrier();
     // 4. records out in tile order: consecutive i of one tile are consecutive
     // records of its global range
     for (int i = threadIdx.x; i < static_cast<int>(total); i += kBinBlock) {
@@ -490,10 +491,10 @@ __global__ void __launch_bounds__(kBinBlock)
       const uint32_t tile = e >> 12, j = e & 0xfffu;
       rec[cursor[tile] + (static_cast<uint32_t>(i) - loff[tile])] = stage[j];
     }
-    __syncthreads();
+    lds_barrier();
     // 5. cursors past this sub-chunk's records
     for (int t = threadIdx.x; t < nt; t += blockDim.x) cursor[t] += loff[t + 1] - loff[t];
-    __syncthreads();
+    lds_barrier();
   }
 
   // non-boundary cells of the slab's empty and split tiles listed by
@@ -810,7 +811,7 @@ __global__ void __launch_bounds__(kTileBlock)
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // B. positions in order of decreasing count (counting sort on
     // min(n, 63)) and the exclusive scan of the counts, one thread per
@@ -834,7 +835,7 @@ __global__ void __launch_bounds__(kTileBlock)
         p_brank = atomicAdd(&bucket[p_bk], 1u);
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < NPOS) {
       uint32_t before = 0;
       for (int w = 0; w < wave; ++w) before += wsum[w];
@@ -850,7 +851,7 @@ __global__ void __launch_bounds__(kTileBlock)
       }
       bstart[tid] = incl - v;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < NPOS) order[bstart[p_bk] + p_brank] = static_cast<uint32_t>(tid);
 
     // C. records in position order; the value tile of a new item (copied by
@@ -867,7 +868,7 @@ __global__ void __launch_bounds__(kTileBlock)
       }
     }
     if (first_of_item) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) only
-    __syncthreads();
+    lds_barrier();
 
     // D. owners: lane group grp takes ranks grp, 2 NG - 1 - grp, 2 NG + grp, ...
     // (snake order: the owners of the largest positions of one round get the
@@ -973,7 +974,7 @@ __global__ void __launch_bounds__(kTileBlock)
       }
     }
     __builtin_amdgcn_s_setprio(0);
-    __syncthreads();
+    lds_barrier();
 
     // E. the next batch's records move into place first (the empty asm
     // pins the wait for their loads here, before this phase's stores and
@@ -1008,7 +1009,7 @@ __global__ void __launch_bounds__(kTileBlock)
     if (next_new_item) stage_value_tile(c1.d);
     c0 = c1;
     c1 = advance(c1);
-    __syncthreads();
+    lds_barrier();
     if (!c0.valid) break;
   }
 }

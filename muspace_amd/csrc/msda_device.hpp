@@ -307,6 +307,20 @@ __device__ __forceinline__ int level_of_sample(int smp, const Shape &s) {
   return static_cast<int>((static_cast<float>(smp) + 0.5f) * s.inv_points);
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wavefront's LDS
+// operations (lgkmcnt) and meets the other wavefronts, but leaves its global
+// loads, stores, atomics and buffer-to-LDS loads in flight. __syncthreads()
+// also drains those (vmcnt(0)), which would turn every prefetch issued before
+// a barrier into a stall at it. Valid where the wavefronts of a workgroup
+// exchange data through LDS only; a buffer-to-LDS load must be waited for
+// (vmcnt) by the wavefront that issued it before this barrier publishes it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left as they are
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Logical block index that gives each XCD a contiguous range of blocks.
 // Workgroups are handed to the 8 XCDs round-robin, so physical block i runs
 // on XCD i % 8; this bijection on [0, nblk) maps XCD x onto the x-th
