@@ -609,12 +609,15 @@ __global__ void __launch_bounds__(kTileBlock)
   constexpr int VPT = (NPOS * UPV + kTileBlock - 1) / kTileBlock;  // value units per thread
   constexpr int RPT = K / kTileBlock;  // records per thread
   constexpr int NR = 4;                // grad_out rows in flight per group
+  // teams of up to 4 groups inside one 16-lane DPP row
+  constexpr int kMaxTeamShift = KQ <= 4 ? 2 : 1;
   static_assert(CPL == 8 && (KQ == 2 || KQ == 4 || KQ == 8), "bad lane layout");
   static_assert(K % kTileBlock == 0 && NPOS <= kTileBlock, "bad batch size");
   static_assert(tile_lds_bytes<VT, C>() + 3400 <= kTileLdsLimit, "tile LDS budget");
 
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
+  __shared__ int team_shift_s;  // log2 of the owner team size of the current batch
   extern __shared__ __align__(16) unsigned char lds[];
   VT *vt = reinterpret_cast<VT *>(lds);  // NPOS cells + one zero row
   float *planes = reinterpret_cast<float *>(lds + static_cast<size_t>(NPOS + 1) * C * VB);
@@ -850,6 +853,14 @@ __global__ void __launch_bounds__(kTileBlock)
         if (tid >= d) incl += up;
       }
       bstart[tid] = incl - v;
+      // owner team size: positions used = NPOS - (positions with count 0)
+      if (tid == kWave - 1) {
+        const int used = NPOS - static_cast<int>(v);
+        int shift = 0;
+        if (kMaxTeamShift >= 1 && used <= NG / 2) shift = 1;
+        if (kMaxTeamShift >= 2 && used <= NG / 4) shift = 2;
+        team_shift_s = shift;
+      }
     }
     lds_barrier();
     if (tid < NPOS) order[bstart[p_bk] + p_brank] = static_cast<uint32_t>(tid);
@@ -870,11 +881,15 @@ __global__ void __launch_bounds__(kTileBlock)
     if (first_of_item) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) only
     lds_barrier();
 
-    // D. owners: lane group grp takes ranks grp, 2 NG - 1 - grp, 2 NG + grp, ...
+    // D. owners: teams of S = 1, 2 or 4 lane groups (inside one 16-lane DPP
+    // row; S grows when the batch uses few positions, as in the thin tiles at
+    // a level's edge); team t takes ranks t, 2 NT - 1 - t, 2 NT + t, ...
     // (snake order: the owners of the largest positions of one round get the
-    // smallest of the next). The first batch of an item visits every position
-    // (zero-count ones store zero sums); later batches stop at the first empty
-    // position and add.
+    // smallest of the next). Group `sub` of a team takes the position's
+    // records sub, sub + S, ...; the S register sums are added across the
+    // team (row_ror) and its last group writes the planes. The first batch of
+    // an item visits every position (zero-count ones store zero sums); later
+    // batches stop at the first empty position and add.
     const VT *gbase =
         grad_out + (static_cast<size_t>(b0) * s.queries * s.heads + m0) * C + k * CPL;
     const uint32_t q_stride = static_cast<uint32_t>(s.heads * C);  // grad_out row stride
@@ -892,9 +907,12 @@ __global__ void __launch_bounds__(kTileBlock)
     } else {
       __builtin_amdgcn_s_setprio(1);
     }
+    const int tshift = team_shift_s;
+    const int S = 1 << tshift, NT = NG >> tshift;
+    const int team = grp >> tshift, sub = grp & (S - 1);
 #pragma unroll 1
-    for (int rnd = 0; rnd * NG < NPOS; ++rnd) {
-      const int i = rnd * NG + ((rnd & 1) ? NG - 1 - grp : grp);
+    for (int rnd = 0; rnd * NT < NPOS; ++rnd) {
+      const int i = rnd * NT + ((rnd & 1) ? NT - 1 - team : team);
       if (i >= NPOS) break;  // later rounds start further out
       const int p_id = static_cast<int>(order[i]);
       const uint32_t n = pcount[p_id];
@@ -904,8 +922,13 @@ __global__ void __launch_bounds__(kTileBlock)
       for (int d = 0; d < 4; ++d)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) acc[d][j] = 0.0f;
-      if (n > 0) {
-        const uint32_t first = poff[p_id];
+      // this group's records of the position: sub, sub + S, ...
+      const uint32_t cnt = n > static_cast<uint32_t>(sub)
+                               ? (n - static_cast<uint32_t>(sub) + S - 1) >> tshift
+                               : 0u;
+      if (cnt > 0) {
+        const uint32_t first = poff[p_id] + static_cast<uint32_t>(sub);
+        const uint32_t stride = static_cast<uint32_t>(S);
         const int py = p_id / TV - 1, px = p_id % TV - 1;  // tile frame, >= -1
         // corner value rows (row -1 or column -1: the zero row after the tile)
         float v[4][CPL];
@@ -933,43 +956,61 @@ __global__ void __launch_bounds__(kTileBlock)
           // D_0..D_3 replace the consumed record (read by this group alone)
           store_corner_dots<KQ>(dd, k, stash_f + slot * 4);
         };
-        // NR records in flight: register set j holds record r + j and is
-        // refilled with record r + j + NR as soon as it is consumed. Past the
-        // end of the list a set keeps its (consumed) record: a processed slot
-        // holds D values, not a record id.
+        // NR records in flight: register set j holds this group's record
+        // r + j and is refilled with record r + j + NR as soon as it is
+        // consumed. Past the end of the list a set keeps its (consumed)
+        // record: a processed slot holds D values, not a record id.
         u32x4 e[NR];
         float g[NR][CPL];
 #pragma unroll
         for (int j = 0; j < NR; ++j) {
-          e[j] = vstash[first + min(static_cast<uint32_t>(j), n - 1)];
+          e[j] = vstash[first + stride * min(static_cast<uint32_t>(j), cnt - 1)];
           load8ch(grow(e[j].x), g[j]);
         }
-        for (uint32_t r = 0; r < n; r += NR) {
+        for (uint32_t r = 0; r < cnt; r += NR) {
 #pragma unroll
           for (int j = 0; j < NR; ++j) {
-            if (r + j < n) one_record(e[j], g[j], first + r + j);
+            if (r + j < cnt) one_record(e[j], g[j], first + stride * (r + j));
             const uint32_t nx = r + j + NR;
-            const u32x4 t = vstash[first + min(nx, n - 1)];
-            e[j] = nx < n ? t : e[j];
+            const u32x4 t = vstash[first + stride * min(nx, cnt - 1)];
+            e[j] = nx < cnt ? t : e[j];
             load8ch(grow(e[j].x), g[j]);
           }
         }
       }
+      // team sum: group g of a row receives group g - 1 (then g - 2), so the
+      // team's last group ends with the sum over the team
+      if (S >= 2) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        float4 *dst = reinterpret_cast<float4 *>(planes + (d * NPOS + p_id) * C + k * CPL);
+        for (int d = 0; d < 4; ++d)
 #pragma unroll
-        for (int h = 0; h < CPL / 4; ++h) {
-          float4 cur = make_float4(acc[d][4 * h], acc[d][4 * h + 1], acc[d][4 * h + 2],
-                                   acc[d][4 * h + 3]);
-          if (!first_of_item) {
-            const float4 old = dst[h];
-            cur.x += old.x;
-            cur.y += old.y;
-            cur.z += old.z;
-            cur.w += old.w;
+          for (int j = 0; j < CPL; ++j) acc[d][j] += MSDA_DPP(acc[d][j], 0x120 + KQ);
+      }
+      if constexpr (kMaxTeamShift >= 2) {
+        if (S >= 4) {
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) acc[d][j] += MSDA_DPP(acc[d][j], 0x120 + 2 * KQ);
+        }
+      }
+      if (sub == S - 1) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          float4 *dst = reinterpret_cast<float4 *>(planes + (d * NPOS + p_id) * C + k * CPL);
+#pragma unroll
+          for (int h = 0; h < CPL / 4; ++h) {
+            float4 cur = make_float4(acc[d][4 * h], acc[d][4 * h + 1], acc[d][4 * h + 2],
+                                     acc[d][4 * h + 3]);
+            if (!first_of_item) {
+              const float4 old = dst[h];
+              cur.x += old.x;
+              cur.y += old.y;
+              cur.z += old.z;
+              cur.w += old.w;
+            }
+            dst[h] = cur;
           }
-          dst[h] = cur;
         }
       }
     }
