@@ -218,15 +218,32 @@ __global__ void __launch_bounds__(kBinBlock)
   const int q0 = ch * p.chunk_q;
   const int nq = min(p.chunk_q, s.queries - q0);
 
-  // samples: consecutive threads read consecutive locations of a query
+  // samples: consecutive threads read consecutive locations of a query; U
+  // samples per thread in flight (every load unconditional, clamped index)
   const int lpp = 1 << p.lp_log2;
-  for (int i = threadIdx.x; i < nq * lpp; i += blockDim.x) {
-    const int q = q0 + (i >> p.lp_log2), smp = i & (lpp - 1);
-    if (smp >= s.lp) continue;
-    const size_t o = (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp;
-    const int l = level_of_sample(smp, s);
-    const Tap t = make_tap(to_float(loc[2 * o]), to_float(loc[2 * o + 1]), lv[l], true);
-    if (t.in) atomicAdd(&hist[primary_tile<T>(t, ntc[l], base[l])], 1u);
+  const int total = nq * lpp;
+  constexpr int U = 8;
+  for (int i0 = threadIdx.x; i0 < total; i0 += kBinBlock * U) {
+    float lx[U], ly[U];
+    bool live[U];
+    int smp[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * kBinBlock;
+      const int q = q0 + (i >> p.lp_log2);
+      smp[u] = i & (lpp - 1);
+      live[u] = i < total && smp[u] < s.lp;
+      const size_t o =
+          live[u] ? (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp[u] : 0;
+      lx[u] = to_float(loc[2 * o]);
+      ly[u] = to_float(loc[2 * o + 1]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int l = level_of_sample(live[u] ? smp[u] : 0, s);
+      const Tap t = make_tap(lx[u], ly[u], lv[l], live[u]);
+      if (t.in) atomicAdd(&hist[primary_tile<T>(t, ntc[l], base[l])], 1u);
+    }
   }
 
   // boundary cells of the slab's tiles ch, ch + chunks, ...
