@@ -53,6 +53,8 @@ constexpr int kBinBlock = 256;           // binning workgroup
 constexpr int kMaxTilesPerSlab = 16384;  // LDS histogram of the binning kernels
 constexpr int kZeroList = 2048;          // tiles listed for zeroing per slab
 constexpr size_t kTileLdsLimit = 160 * 1024;
+constexpr int kXcdQueues = 8;            // item queues of the tile kernel (one per XCD)
+constexpr uint32_t kNoItem = 0xffffffffu;
 
 // Host-computed sizes of the binning scratch (all per (b, m) slab).
 struct BinPlan {
@@ -210,7 +212,8 @@ __global__ void __launch_bounds__(kBinBlock)
   stage_tiles<T>(lv, s.levels, ntc, base);
   const int nt = base[s.levels];
   for (int i = threadIdx.x; i < nt; i += blockDim.x) hist[i] = 0;
-  if (blockIdx.x == 0 && threadIdx.x == 0) *item_total = 0;
+  // the item counter and the tile kernel's per-XCD take counters
+  if (blockIdx.x == 0 && threadIdx.x <= kXcdQueues) item_total[threadIdx.x] = 0;
   __syncthreads();
 
   const int bm = blockIdx.x / p.chunks, ch = blockIdx.x % p.chunks;
@@ -614,7 +617,7 @@ __global__ void __launch_bounds__(kTileBlock)
     msda_tile_backward(const VT *__restrict__ value, uint32_t value_bytes,
                        const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                        const VT *__restrict__ grad_out, uint4 *__restrict__ records,
-                       const Item *__restrict__ items, const uint32_t *__restrict__ item_total,
+                       const Item *__restrict__ items, uint32_t *__restrict__ item_total,
                        Shape s, BinPlan p, float *__restrict__ grad_value) {
   using Cfg = TileCfg<VT, C>;
   constexpr int T = Cfg::T, K = Cfg::K, CPL = Cfg::CPL;
@@ -655,29 +658,48 @@ __global__ void __launch_bounds__(kTileBlock)
   const int grp = tid / KQ, k = tid % KQ;
   const __amdgpu_buffer_rsrc_t vrsrc = make_rsrc(value, value_bytes);
 
-  // this workgroup's items: lo + wid, lo + wid + nw, ... below hi
-  constexpr int kXcd = 8;
+  // Items are taken dynamically: the list is cut into one contiguous share
+  // per XCD (workgroups are dispatched to the XCDs round-robin, so block
+  // i % 8 runs on XCD i % 8 and a slab's items stay in one XCD's L2), and
+  // the workgroups of an XCD take items of its share in list order through
+  // an atomic counter (zeroed by bin_count). Thread 0 takes the next item one
+  // item ahead and publishes its index through LDS.
   const uint32_t n_items = min(*item_total, static_cast<uint32_t>(p.item_cap));
-  const int xcd = blockIdx.x % kXcd, wid = blockIdx.x / kXcd, nw = gridDim.x / kXcd;
-  const uint32_t lo = static_cast<uint32_t>(static_cast<uint64_t>(n_items) * xcd / kXcd);
-  const uint32_t hi = static_cast<uint32_t>(static_cast<uint64_t>(n_items) * (xcd + 1) / kXcd);
-  auto item_at = [&](int n, bool &ok) {
-    const uint64_t idx = static_cast<uint64_t>(lo) + wid + static_cast<uint64_t>(n) * nw;
-    ok = idx < hi;
+  const int xcd = static_cast<int>(blockIdx.x % kXcdQueues);
+  const uint32_t lo = static_cast<uint32_t>(static_cast<uint64_t>(n_items) * xcd / kXcdQueues);
+  const uint32_t hi =
+      static_cast<uint32_t>(static_cast<uint64_t>(n_items) * (xcd + 1) / kXcdQueues);
+  uint32_t *queue = item_total + 1 + xcd;
+  __shared__ uint32_t taken[2];
+  auto take_item = [&]() -> uint32_t {  // thread 0 only
+    const uint32_t i = lo < hi ? atomicAdd(queue, 1u) : 0u;
+    return lo + i < hi ? lo + i : kNoItem;
+  };
+  auto item_of = [&](uint32_t idx, bool &ok) {
+    ok = idx != kNoItem;
     Item d{0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
     if (ok) d = items[idx];
     return d;
   };
 
   // cursors of batches b (c0) and b + 1 (c1); `pre` is the descriptor of the
-  // item after c1's
+  // item after c1's. advance() hands `pre` over when a cursor moves to a new
+  // item; the caller then refills `pre` from a freshly taken item.
+  if (tid == 0) {
+    taken[0] = take_item();
+    taken[1] = take_item();
+  }
+  __syncthreads();
   BatchCursor c0;
   c0.n = 0;
   c0.k = 0;
-  c0.d = item_at(0, c0.valid);
+  c0.d = item_of(taken[0], c0.valid);
   if (!c0.valid) return;  // uniform: no item for this workgroup
   bool pre_ok;
-  Item pre = item_at(1, pre_ok);
+  Item pre = item_of(taken[1], pre_ok);
+  auto moves_on = [&](const BatchCursor &c) {
+    return c.valid && c.k + 1 >= item_batches<K>(c.d);
+  };
   auto advance = [&](const BatchCursor &c) {
     BatchCursor r = c;
     if (!c.valid) return r;
@@ -688,11 +710,15 @@ __global__ void __launch_bounds__(kTileBlock)
       r.k = 0;
       r.d = pre;
       r.valid = pre_ok;
-      pre = item_at(r.n + 1, pre_ok);
     }
     return r;
   };
+  const bool refill0 = moves_on(c0);
+  __syncthreads();  // taken[] read by every thread
+  if (refill0 && tid == 0) taken[0] = take_item();
   BatchCursor c1 = advance(c0);
+  __syncthreads();
+  if (refill0) pre = item_of(taken[0], pre_ok);
 
   auto batch_range = [&](const BatchCursor &c, uint32_t &s0, uint32_t &s1) {
     s0 = c.d.r0 + c.k * K;
@@ -801,6 +827,13 @@ __global__ void __launch_bounds__(kTileBlock)
     const bool last_of_item = c0.k + 1 == item_batches<K>(c0.d);
     const bool next_new_item = c1.valid && c1.k == 0;
     const int b0 = static_cast<int>(c0.d.b), m0 = static_cast<int>(c0.d.m);
+
+    // c1 moves on to a new item at the end of this batch: thread 0 takes
+    // the item after it now and publishes it in phase E, so the atomic's
+    // round trip overlaps the batch
+    const bool refill = moves_on(c1);
+    uint32_t took = 0;
+    if (refill && tid == 0 && lo < hi) took = atomicAdd(queue, 1u);
 
     // A. next batch's records; this batch's sort keys. Record slots are
     // u * kTileBlock + tid; a wavefront whose first slot is past the batch
@@ -1065,9 +1098,11 @@ __global__ void __launch_bounds__(kTileBlock)
     if (tid < kWave) bucket[tid] = 0;
     if (last_of_item) write_back(c0.d);
     if (next_new_item) stage_value_tile(c1.d);
+    if (refill && tid == 0) taken[0] = lo + took < hi ? lo + took : kNoItem;
     c0 = c1;
     c1 = advance(c1);
     lds_barrier();
+    if (refill) pre = item_of(taken[0], pre_ok);
     if (!c0.valid) break;
   }
 }

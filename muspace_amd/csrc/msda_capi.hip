@@ -402,7 +402,7 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   w.records = take(static_cast<size_t>(bm) * p.rec_cap * 16);
   w.rec_of_sample = take(static_cast<size_t>(bm) * p.rec_cap * 4);
   w.items = take(static_cast<size_t>(p.item_cap) * sizeof(msda::Item));
-  w.item_total = take(4);
+  w.item_total = take(4 * (1 + msda::kXcdQueues));  // item count, per-XCD take counters
   w.bytes = off;
   return true;
 }
