@@ -20,8 +20,10 @@
 //                  holding more ("split"); items appended, coarsest level
 //                  first, to one compact list; zeroes the cells of empty and
 //                  split tiles and the value rows that belong to no level.
-//   3. bin_scatter per chunk: 16-byte records {query<<lp_log2 | sample,
-//                  location x, location y, attention weight} into their tile.
+//   3. bin_scatter per chunk: 16-byte records {position << 23 | query <<
+//                  lp_log2 | sample, wx1, wy1, attention weight} into their
+//                  tile (position: the top-left corner in the tile frame;
+//                  wx1, wy1: the bilinear fractions of the sample's tap).
 //   4. tile        persistent, one 1024-thread workgroup per CU, items taken
 //                  round-robin inside an XCD's share of the list: stage the
 //                  value tile in LDS, then for each batch of K records:
@@ -54,6 +56,8 @@ constexpr int kMaxTilesPerSlab = 16384;  // LDS histogram of the binning kernels
 constexpr int kZeroList = 2048;          // tiles listed for zeroing per slab
 constexpr size_t kTileLdsLimit = 160 * 1024;
 constexpr int kXcdQueues = 8;            // item queues of the tile kernel (one per XCD)
+constexpr int kPosShift = 23;            // record id bits [23, 32): position in the tile frame
+constexpr uint32_t kSampleMask = (1u << kPosShift) - 1u;  // (q << lp_log2) | sample
 constexpr uint32_t kNoItem = 0xffffffffu;
 
 // Host-computed sizes of the binning scratch (all per (b, m) slab).
@@ -61,7 +65,7 @@ struct BinPlan {
   int chunks;       // query chunks per slab
   int chunk_q;      // queries per chunk
   int tile_bound;   // stride of the per-slab tile arrays (>= tiles per slab)
-  int lp_log2;      // record id = (q << lp_log2) | sample
+  int lp_log2;      // record id = (position << kPosShift) | (q << lp_log2) | sample
   int rmax;         // records per work item (a multiple of the batch size)
   int item_cap;     // capacity of the compact work-item list (all slabs)
   int64_t rec_cap;  // records per slab = queries * lp (one per sample)
@@ -475,8 +479,13 @@ __global__ void __launch_bounds__(kBinBlock)
         const uint32_t rank = atomicAdd(&loff[tile], 1u);
         key[u] = (static_cast<uint32_t>(tile) << 12) | static_cast<uint32_t>(j);
         at = cursor[tile] + rank;
-        stage[j] = make_uint4((static_cast<uint32_t>(q) << p.lp_log2) | static_cast<uint32_t>(smp),
-                              __float_as_uint(lx[u]), __float_as_uint(ly[u]),
+        // top-left corner in the frame of its primary tile: [-1, T-1]^2 -> [0, T]^2
+        const int ty = t.y0 < 0 ? 0 : t.y0, tx = t.x0 < 0 ? 0 : t.x0;
+        const int pos = (t.y0 - (ty / T) * T + 1) * (T + 1) + (t.x0 - (tx / T) * T + 1);
+        stage[j] = make_uint4((static_cast<uint32_t>(pos) << kPosShift) |
+                                  (static_cast<uint32_t>(q) << p.lp_log2) |
+                                  static_cast<uint32_t>(smp),
+                              __float_as_uint(t.wx1), __float_as_uint(t.wy1),
                               __float_as_uint(aw[u]));
         rk[u] = rank;
       }
@@ -852,16 +861,12 @@ __global__ void __launch_bounds__(kTileBlock)
       rank[u] = 0;
       my_wx1[u] = my_wy1[u] = 0.0f;
       my_a[u] = __uint_as_float(r_cur[u].w);
-      if (wave_slot + u * kTileBlock < ns) {
-        const Tap t =
-            make_tap(__uint_as_float(r_cur[u].y), __uint_as_float(r_cur[u].z), L, i < ns);
-        const int py = t.y0 - g0.y_lo + 1, px = t.x0 - g0.x_lo + 1;
-        my_wx1[u] = t.wx1;
-        my_wy1[u] = t.wy1;
-        if (t.in && py >= 0 && py < TV && px >= 0 && px < TV) {  // always, for binned records
-          pos[u] = py * TV + px;
-          rank[u] = atomicAdd(&pcount[pos[u]], 1u);
-        }
+      // the record carries its tap (bin_scatter): position, wx1, wy1
+      if (wave_slot + u * kTileBlock < ns && i < ns) {
+        my_wx1[u] = __uint_as_float(r_cur[u].y);
+        my_wy1[u] = __uint_as_float(r_cur[u].z);
+        pos[u] = static_cast<int>(min(r_cur[u].x >> kPosShift, static_cast<uint32_t>(NPOS - 1)));
+        rank[u] = atomicAdd(&pcount[pos[u]], 1u);
       }
     }
     lds_barrier();
@@ -947,7 +952,8 @@ __global__ void __launch_bounds__(kTileBlock)
     float *stash_f = reinterpret_cast<float *>(stash);
     // q < 2^24 and q * q_stride < 2^32 (checked on the host): a 24-bit multiply
     auto grow = [&](uint32_t id) {
-      const uint32_t q = min(id >> p.lp_log2, static_cast<uint32_t>(s.queries - 1));
+      const uint32_t q =
+          min((id & kSampleMask) >> p.lp_log2, static_cast<uint32_t>(s.queries - 1));
       return gbase + __umul24(q, q_stride);
     };
     // Round 0 hands the largest positions to the lowest wavefronts; they get

@@ -382,7 +382,10 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   if (msda::scatter_lds_bytes(p.tile_bound) + 4096 > msda::kTileLdsLimit) return false;
   p.lp_log2 = log2_int(s.lp > 0 ? s.lp : 1);
   if ((1 << p.lp_log2) > msda::kScatterSlots) return false;
-  if ((static_cast<int64_t>(s.queries) << p.lp_log2) > (int64_t{1} << 32)) return false;
+  // record ids pack (q << lp_log2) | sample below bit kPosShift and the tap's
+  // position in the tile frame above it
+  if ((static_cast<int64_t>(s.queries) << p.lp_log2) > (int64_t{1} << msda::kPosShift)) return false;
+  if ((T + 1) * (T + 1) > (1 << (32 - msda::kPosShift))) return false;
   // the tile kernel addresses grad_out rows with a 24-bit multiply (q < 2^24)
   // and a 32-bit element offset inside one batch entry
   if (s.queries >= (1 << 24)) return false;
