@@ -396,12 +396,16 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   p.rec_cap = static_cast<int64_t>(s.queries) * s.lp;
   if (p.rec_cap >= (int64_t{1} << 31)) return false;
   const int64_t bm = static_cast<int64_t>(s.batch) * s.heads;
-  // records per work item: about 16 items per workgroup, in whole batches
+  // records per work item (a tile with more is split into items whose cells
+  // are all added atomically): about 4 items' worth per workgroup, 4 to 8
+  // batches, in whole batches. Measured at the benchmark shapes: single-
+  // batch items (splitting nearly every tile) cost c1 55 us; items of more
+  // than 8 batches leave the largest ones running alone at the end (c4).
   const int K = tile_batch(value_dtype, s.channels);
   const int64_t total = bm * p.rec_cap;
   if (total >= (int64_t{1} << 32)) return false;  // sample indices are 32-bit in the tile kernel
-  int64_t mult = (total + int64_t{16} * tile_grid() * K - 1) / (int64_t{16} * tile_grid() * K);
-  mult = mult < 1 ? 1 : (mult > 64 ? 64 : mult);
+  int64_t mult = (total + int64_t{4} * tile_grid() * K - 1) / (int64_t{4} * tile_grid() * K);
+  mult = mult < 4 ? 4 : (mult > 8 ? 8 : mult);
   p.rmax = static_cast<int>(mult * K);
   const int64_t item_cap = bm * (p.tile_bound + (p.rec_cap + p.rmax - 1) / p.rmax + 1);
   if (item_cap >= (int64_t{1} << 31)) return false;
