@@ -90,7 +90,7 @@ constexpr uint32_t kTileIndexMask = 0xffffu;
 template <typename VT, int C>
 struct TileCfg;
 template <> struct TileCfg<float, 16> { static constexpr int T = 16, K = 2048, CPL = 8; };
-template <> struct TileCfg<float, 32> { static constexpr int T = 12, K = 2048, CPL = 8; };
+template <> struct TileCfg<float, 32> { static constexpr int T = 13, K = 1536, CPL = 8; };
 template <> struct TileCfg<float, 64> { static constexpr int T = 8, K = 2048, CPL = 8; };
 template <> struct TileCfg<bf16_t, 16> { static constexpr int T = 16, K = 2048, CPL = 8; };
 template <> struct TileCfg<bf16_t, 32> { static constexpr int T = 13, K = 2048, CPL = 8; };
