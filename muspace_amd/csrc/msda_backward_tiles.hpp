@@ -637,7 +637,7 @@ __global__ void __launch_bounds__(kTileBlock)
   constexpr int UPV = C * VB / 16;     // 16-byte units per value row
   constexpr int VPT = (NPOS * UPV + kTileBlock - 1) / kTileBlock;  // value units per thread
   constexpr int RPT = K / kTileBlock;  // records per thread
-  constexpr int NR = 4;                // grad_out rows in flight per group
+  constexpr int NR = 2;                // grad_out rows in flight per group
   // teams of up to 4 groups inside one 16-lane DPP row
   constexpr int kMaxTeamShift = KQ <= 4 ? 2 : 1;
   static_assert(CPL == 8 && (KQ == 2 || KQ == 4 || KQ == 8), "bad lane layout");
