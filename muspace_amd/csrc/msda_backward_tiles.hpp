@@ -956,13 +956,6 @@ __global__ void __launch_bounds__(kTileBlock)
           min((id & kSampleMask) >> p.lp_log2, static_cast<uint32_t>(s.queries - 1));
       return gbase + __umul24(q, q_stride);
     };
-    // Round 0 hands the largest positions to the lowest wavefronts; they get
-    // issue priority over the wavefronts they share a SIMD with.
-    if (wave < kTileBlock / kWave / 2) {
-      __builtin_amdgcn_s_setprio(2);
-    } else {
-      __builtin_amdgcn_s_setprio(1);
-    }
     const int tshift = team_shift_s;
     const int S = 1 << tshift, NT = NG >> tshift;
     const int team = grp >> tshift, sub = grp & (S - 1);
@@ -1070,7 +1063,6 @@ __global__ void __launch_bounds__(kTileBlock)
         }
       }
     }
-    __builtin_amdgcn_s_setprio(0);
     lds_barrier();
 
     // E. the next batch's records move into place first (the empty asm
