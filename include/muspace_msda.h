@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define MUSPACE_MSDA_ABI_VERSION 1
+#define MUSPACE_MSDA_ABI_VERSION 2
 
 /* the library is built with -fvisibility=hidden; only these symbols export */
 #if defined(__GNUC__)
@@ -118,6 +118,50 @@ MUSPACE_API int ms_deform_attn_backward_ws(
     int64_t batch, int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
     int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
     size_t workspace_bytes, void *stream);
+
+/* BEVFormer spatial cross-attention, one camera, with the scatter-average
+ * fused into the forward: for the camera-rebatched
+ *   value               [batch*num_cams, spatial_size, num_heads, channels]  value_dtype
+ *   sampling_locations  [batch*num_cams, max_len, num_heads, num_levels, num_point, 2]
+ *   attention_weights   [batch*num_cams, max_len, num_heads, num_levels, num_point]
+ * (row b*num_cams + cam_id holds camera cam_id of batch b; geometry_dtype), the
+ * BEV query of each of the camera's rows
+ *   index               [valid_len] int64 (distinct; entries outside
+ *                       [0, num_query) are skipped)
+ * and the per-query camera count
+ *   count               [batch, num_query] geometry_dtype (>= 1)
+ * it adds, for every b, r < valid_len, head m and channel c,
+ *   slots[b, index[r], m*channels + c] += MSDA(b*num_cams + cam_id, r, m, c) / count[b, index[r]]
+ * to slots [batch, num_query, num_heads*channels] value_dtype, in place.
+ * Rows r >= valid_len (the rebatch padding) are not read. Calls for different
+ * cameras of the same slots must be ordered (same stream): a camera's rows
+ * are added without atomics. Replaces the reference's unexported
+ * ms_deformable_im2col_scatter_div_musa
+ * (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:455-505, kernel
+ * ms_deform_attn_musa_kernel.muh:419-486), same arguments and order plus the
+ * dtype codes; any channel count (the reference's supports 32 only). */
+MUSPACE_API int ms_deform_attn_forward_scatter_div(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_weights, int geometry_dtype, const int64_t *index, const void *count,
+    void *slots, int64_t batch, int64_t num_cams, int64_t cam_id, int64_t valid_len,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t max_len, int64_t num_point, int64_t num_query, void *stream);
+
+/* Gradient of ms_deform_attn_forward_scatter_div's MSDA output rows for one
+ * camera: grad_output[b*num_cams + cam_id, r, :] = grad_slots[b, index[r], :] /
+ * count[b, index[r]] for r < valid_len, zero for valid_len <= r < max_len and
+ * for skipped indices. grad_slots [batch, num_query, row] and grad_output
+ * [batch*num_cams, max_len, row] are value_dtype; count is float32 or
+ * value_dtype. ms_deform_attn_backward on grad_output then gives the value,
+ * location and weight gradients. No reference counterpart (the reference's
+ * fused path is forward-only); it is the chain rule of the same sum. */
+MUSPACE_API int ms_deform_attn_scatter_div_grad(const void *grad_slots, int value_dtype,
+                                                const int64_t *index, const void *count,
+                                                int count_dtype, void *grad_output,
+                                                int64_t batch, int64_t num_cams, int64_t cam_id,
+                                                int64_t valid_len, int64_t max_len,
+                                                int64_t num_query, int64_t row, void *stream);
 
 /* Build smoke: y[i] = x[i] + 1 for i < n (float32). Mirrors add_one
  * (/root/reference/csrc/ffi/muspace_ops.mu:40-55). */

@@ -11,6 +11,7 @@ from .ops import (
     multi_scale_deformable_attn,
     multi_scale_deformable_attn_pytorch,
     multi_scale_deformable_attn_pytorch_compat,
+    multi_scale_deformable_attn_scatter_div,
 )
 from .runtime.kernel_dispatch import (
     DispatchDecision,
@@ -33,4 +34,5 @@ __all__ = [
     "multi_scale_deformable_attn",
     "multi_scale_deformable_attn_pytorch",
     "multi_scale_deformable_attn_pytorch_compat",
+    "multi_scale_deformable_attn_scatter_div",
 ]

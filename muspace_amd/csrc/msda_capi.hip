@@ -190,41 +190,41 @@ bool rows_aligned(std::initializer_list<const void *> ptrs16, const void *ptr8 =
 
 // ---------------------------------------------------------------- forward ---
 
+// Runs go(NS, launch) with NS the samples per lane group that plan_rows chose
+// for the forward row kernels (1, 2, 4 or 8, at most KQ).
+template <typename VT, int C, typename Go>
+void forward_rows_ns(const msda::Shape &s, Go &&go) {
+  constexpr int KQ = C / msda::RowTraits<VT>::kCpl;
+  const Launch L = plan_rows(s, KQ, 8);
+  switch (L.ns) {
+    case 1:
+      go(std::integral_constant<int, 1>(), L);
+      break;
+    case 2:
+      if constexpr (KQ >= 2) go(std::integral_constant<int, 2>(), L);
+      break;
+    case 8:
+      if constexpr (KQ >= 8) go(std::integral_constant<int, 8>(), L);
+      break;
+    default:
+      if constexpr (KQ >= 4) go(std::integral_constant<int, 4>(), L);
+      break;
+  }
+}
+
 template <typename VT, typename GT, int C>
 void launch_forward_rows(const void *value, const int64_t *shapes, const int64_t *starts,
                          const void *loc, const void *attn, void *out, const msda::Shape &s,
                          hipStream_t st) {
-  constexpr int KQ = C / msda::RowTraits<VT>::kCpl;
-  const Launch L = plan_rows(s, KQ, 8);
   const VT *v = static_cast<const VT *>(value);
   const GT *lc = static_cast<const GT *>(loc);
   const GT *aw = static_cast<const GT *>(attn);
   VT *o = static_cast<VT *>(out);
   const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
-  switch (L.ns) {
-    case 1:
-      msda::msda_forward_rows<VT, GT, C, 1>
-          <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, o, s, L.plan);
-      break;
-    case 2:
-      if constexpr (KQ >= 2) {
-        msda::msda_forward_rows<VT, GT, C, 2>
-            <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, o, s, L.plan);
-      }
-      break;
-    case 8:
-      if constexpr (KQ >= 8) {
-        msda::msda_forward_rows<VT, GT, C, 8>
-            <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, o, s, L.plan);
-      }
-      break;
-    default:
-      if constexpr (KQ >= 4) {
-        msda::msda_forward_rows<VT, GT, C, 4>
-            <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, o, s, L.plan);
-      }
-      break;
-  }
+  forward_rows_ns<VT, C>(s, [&](auto ns, const Launch &L) {
+    msda::msda_forward_rows<VT, GT, C, decltype(ns)::value>
+        <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, o, s, L.plan);
+  });
 }
 
 template <typename VT, typename GT>
@@ -249,6 +249,117 @@ void launch_forward(const void *value, const int64_t *shapes, const int64_t *sta
           <<<generic_blocks(static_cast<int64_t>(s.units) * s.channels), msda::kBlock, 0, st>>>(
               static_cast<const VT *>(value), shapes, starts, static_cast<const GT *>(loc),
               static_cast<const GT *>(attn), static_cast<VT *>(out), s);
+      return;
+  }
+}
+
+// ------------------------------------------ spatial cross-attention epilogue ---
+
+// Camera-rebatched dims of the scatter-average entry points.
+struct CamArgs {
+  int64_t batch, cams, cam, valid_len, max_len, num_query;
+};
+
+// Validates the fused scatter-average call and fills `s` for one camera:
+// s.batch = batch, s.queries = valid_len (the units this launch computes).
+// `full` describes the whole rebatched value and geometry.
+int validate_cameras(const char *fn, const Args &a, const CamArgs &c, int value_dtype,
+                     int geometry_dtype, msda::Shape &s, msda::Shape &full) {
+  if (c.batch < 0 || c.cams <= 0 || c.cam < 0 || c.cam >= c.cams || c.max_len < 0 ||
+      c.valid_len < 0 || c.valid_len > c.max_len || c.num_query < 0) {
+    return fail(MUSPACE_EINVAL,
+                "%s: invalid dims batch=%lld num_cams=%lld cam_id=%lld valid_len=%lld "
+                "max_len=%lld num_query=%lld (need 0 <= cam_id < num_cams and "
+                "0 <= valid_len <= max_len)",
+                fn, (long long)c.batch, (long long)c.cams, (long long)c.cam,
+                (long long)c.valid_len, (long long)c.max_len, (long long)c.num_query);
+  }
+  if (c.batch * c.cams > INT_MAX) {
+    return fail(MUSPACE_ERANGE, "%s: batch*num_cams exceeds int32", fn);
+  }
+  if (int rc = validate(fn, a, value_dtype, geometry_dtype, full)) return rc;
+  s = full;
+  s.batch = static_cast<int>(c.batch);
+  s.queries = static_cast<int>(c.valid_len);
+  s.units = static_cast<int>(c.batch * c.valid_len * a.heads);
+  return ok();
+}
+
+template <typename VT, typename GT>
+void launch_scatter_div(const void *value, const int64_t *shapes, const int64_t *starts,
+                        const void *loc, const void *attn, const msda::ScatterAverage<VT, GT> &out,
+                        const msda::Shape &s, const msda::Shape &full, void *slots,
+                        hipStream_t st) {
+  const VT *v = static_cast<const VT *>(value);
+  const GT *lc = static_cast<const GT *>(loc);
+  const GT *aw = static_cast<const GT *>(attn);
+  // the row kernel addresses all cameras' value with 32-bit byte offsets
+  const size_t vb = value_bytes(full, sizeof(VT));
+  const bool small = vb + 64 <= msda::kOobOffset;
+  const int rows = rows_aligned({value, slots}) && small ? s.channels : 0;
+  const uint32_t vbytes = static_cast<uint32_t>(vb);
+  auto go = [&](auto cc) {
+    constexpr int C = decltype(cc)::value;
+    forward_rows_ns<VT, C>(s, [&](auto ns, const Launch &L) {
+      msda::msda_forward_scatter_div_rows<VT, GT, C, decltype(ns)::value>
+          <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, out, s, L.plan);
+    });
+  };
+  switch (rows) {
+    case 16: go(std::integral_constant<int, 16>()); return;
+    case 32: go(std::integral_constant<int, 32>()); return;
+    case 64: go(std::integral_constant<int, 64>()); return;
+    default:
+      msda::msda_forward_scatter_div_generic<VT, GT>
+          <<<generic_blocks(static_cast<int64_t>(s.units) * s.channels), msda::kBlock, 0, st>>>(
+              v, shapes, starts, lc, aw, out, s);
+      return;
+  }
+}
+
+template <typename VT, typename GT>
+void launch_scatter_div_grad(const void *grad_slots, const int64_t *index, const void *count,
+                             void *grad_out, const CamArgs &c, int row, hipStream_t st) {
+  constexpr int W = 16 / static_cast<int>(sizeof(VT));
+  const VT *g = static_cast<const VT *>(grad_slots);
+  const GT *cnt = static_cast<const GT *>(count);
+  VT *o = static_cast<VT *>(grad_out);
+  const bool vec = row % W == 0 && aligned(grad_slots, 16) && aligned(grad_out, 16);
+  const int64_t work = c.batch * c.max_len * (vec ? row / W : row);
+  const int B = static_cast<int>(c.batch), NC = static_cast<int>(c.cams),
+            cam = static_cast<int>(c.cam), V = static_cast<int>(c.valid_len),
+            ML = static_cast<int>(c.max_len), NQ = static_cast<int>(c.num_query);
+  if (vec) {
+    msda::msda_scatter_div_grad<VT, GT, W><<<generic_blocks(work), msda::kBlock, 0, st>>>(
+        g, index, cnt, o, B, NC, cam, V, ML, NQ, row);
+  } else {
+    msda::msda_scatter_div_grad<VT, GT, 1><<<generic_blocks(work), msda::kBlock, 0, st>>>(
+        g, index, cnt, o, B, NC, cam, V, ML, NQ, row);
+  }
+}
+
+// Calls f(VT(), GT()) for the value dtype and the geometry (loc, attn, count)
+// dtype: float32 or the value dtype.
+template <typename F>
+void with_dtypes(int value_dtype, int geometry_dtype, F &&f) {
+  using msda::bf16_t;
+  switch (value_dtype) {
+    case MUSPACE_DTYPE_F32:
+      f(float(), float());
+      return;
+    case MUSPACE_DTYPE_F16:
+      if (geometry_dtype == MUSPACE_DTYPE_F32) {
+        f(__half(), float());
+      } else {
+        f(__half(), __half());
+      }
+      return;
+    default:
+      if (geometry_dtype == MUSPACE_DTYPE_F32) {
+        f(bf16_t(), float());
+      } else {
+        f(bf16_t(), bf16_t());
+      }
       return;
   }
 }
@@ -615,6 +726,78 @@ int ms_deform_attn_forward(const void *value, int value_dtype, const int64_t *sp
       }
       break;
   }
+  return check_launch(fn);
+}
+
+int ms_deform_attn_forward_scatter_div(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_weights, int geometry_dtype, const int64_t *index, const void *count,
+    void *slots, int64_t batch, int64_t num_cams, int64_t cam_id, int64_t valid_len,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t max_len, int64_t num_point, int64_t num_query, void *stream) {
+  static const char *fn = "ms_deform_attn_forward_scatter_div";
+  const int64_t rows = batch * num_cams;
+  const Args a{rows, spatial_size, num_heads, channels, num_levels, max_len, num_point,
+               rows > 0 ? rows : 1};
+  const CamArgs c{batch, num_cams, cam_id, valid_len, max_len, num_query};
+  msda::Shape s, full;
+  if (int rc = validate_cameras(fn, a, c, value_dtype, geometry_dtype, s, full)) return rc;
+  if (!needs_data(s) || s.lp == 0) return ok();  // nothing is added to the slots
+  if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+      !attention_weights || !index || !count || !slots) {
+    return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+  }
+  const int cams = static_cast<int>(num_cams), cam = static_cast<int>(cam_id),
+            ml = static_cast<int>(max_len), nq = static_cast<int>(num_query);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  with_dtypes(value_dtype, geometry_dtype, [&](auto vt, auto gt) {
+    using VT = decltype(vt);
+    using GT = decltype(gt);
+    const msda::ScatterAverage<VT, GT> out{static_cast<VT *>(slots), index,
+                                           static_cast<const GT *>(count), cams, cam, ml, nq};
+    launch_scatter_div<VT, GT>(value, spatial_shapes, level_start_index, sampling_locations,
+                               attention_weights, out, s, full, slots, st);
+  });
+  return check_launch(fn);
+}
+
+int ms_deform_attn_scatter_div_grad(const void *grad_slots, int value_dtype,
+                                    const int64_t *index, const void *count, int count_dtype,
+                                    void *grad_output, int64_t batch, int64_t num_cams,
+                                    int64_t cam_id, int64_t valid_len, int64_t max_len,
+                                    int64_t num_query, int64_t row, void *stream) {
+  static const char *fn = "ms_deform_attn_scatter_div_grad";
+  if (value_dtype != MUSPACE_DTYPE_F32 && value_dtype != MUSPACE_DTYPE_F16 &&
+      value_dtype != MUSPACE_DTYPE_BF16) {
+    return fail(MUSPACE_EINVAL, "%s: grad must be float32, float16 or bfloat16 (dtype code %d)",
+                fn, value_dtype);
+  }
+  if (count_dtype != MUSPACE_DTYPE_F32 && count_dtype != value_dtype) {
+    return fail(MUSPACE_EINVAL, "%s: count must be float32 or %s, got %s", fn,
+                dtype_name(value_dtype), dtype_name(count_dtype));
+  }
+  const CamArgs c{batch, num_cams, cam_id, valid_len, max_len, num_query};
+  if (batch < 0 || num_cams <= 0 || cam_id < 0 || cam_id >= num_cams || max_len < 0 ||
+      valid_len < 0 || valid_len > max_len || num_query < 0 || row <= 0) {
+    return fail(MUSPACE_EINVAL,
+                "%s: invalid dims batch=%lld num_cams=%lld cam_id=%lld valid_len=%lld "
+                "max_len=%lld num_query=%lld row=%lld",
+                fn, (long long)batch, (long long)num_cams, (long long)cam_id,
+                (long long)valid_len, (long long)max_len, (long long)num_query, (long long)row);
+  }
+  if (batch * num_cams > INT_MAX || max_len > INT_MAX || num_query > INT_MAX || row > INT_MAX) {
+    return fail(MUSPACE_ERANGE, "%s: dims exceed int32", fn);
+  }
+  if (batch == 0 || max_len == 0) return ok();
+  if (!grad_output || (valid_len > 0 && (!grad_slots || !index || !count))) {
+    return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  with_dtypes(value_dtype, count_dtype, [&](auto vt, auto gt) {
+    launch_scatter_div_grad<decltype(vt), decltype(gt)>(grad_slots, index, count, grad_output, c,
+                                                        static_cast<int>(row), st);
+  });
   return check_launch(fn);
 }
 

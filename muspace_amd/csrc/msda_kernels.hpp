@@ -78,6 +78,81 @@ __device__ __forceinline__ Unit decode_unit(int u, const Shape &s) {
 
 // ------------------------------------------------------------- forward ---
 
+// Where a forward unit (b, q, m) reads its geometry and value, and what it does
+// with its C sums.
+//
+// DenseRows: the operator's output, out[(b*nq + q)*M + m][C]; geometry row
+// (b, q, m) of [batch, nq, M, L*P]; value slab b of [batch, spatial, M, C].
+template <typename VT>
+struct DenseRows {
+  VT *out;
+  __device__ __forceinline__ int geo_row(int b, int q, int m, const Shape &s) const {
+    return (b * s.queries + q) * s.heads + m;
+  }
+  __device__ __forceinline__ size_t slab(int b, const Shape &s) const {
+    return static_cast<size_t>(b) * s.spatial;
+  }
+  template <int C, int CPL>
+  __device__ __forceinline__ void put(int b, int q, int m, int k, const float (&acc)[CPL],
+                                      const Shape &s) const {
+    store16(out + static_cast<size_t>(geo_row(b, q, m, s)) * C + k * CPL, acc);
+  }
+  __device__ __forceinline__ void put1(int b, int q, int m, int c, float acc,
+                                       const Shape &s) const {
+    out[static_cast<size_t>(geo_row(b, q, m, s)) * s.channels + c] = from_float<VT>(acc);
+  }
+};
+
+// ScatterAverage: BEVFormer spatial cross-attention's epilogue for one camera,
+// fused into the forward (reference sketch: ms_deformable_im2col_scatter_div_*,
+// /root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa_kernel.muh:419-486).
+// Value and geometry are camera-rebatched, [batch*cams, spatial, M, C] and
+// [batch*cams, max_len, M, L*P]; unit (b, q, m) is row q < valid_len of camera
+// `cam` in batch b, and its sums are added to the BEV query index[q]:
+//   slots[b, index[q], m*C + c] += sum_c * (1 / count[b, index[q]]).
+// A camera's indices are distinct (one launch adds each slot at most once), so
+// the read-modify-write needs no atomics; cameras are launched in order. An
+// index outside [0, num_query) adds nothing.
+template <typename VT, typename CT>
+struct ScatterAverage {
+  VT *slots;             // [batch, num_query, M*C]
+  const int64_t *index;  // [valid_len] BEV query of each row of this camera
+  const CT *count;       // [batch, num_query], cameras that see the query
+  int cams, cam, max_len, num_query;
+  __device__ __forceinline__ int geo_row(int b, int q, int m, const Shape &s) const {
+    return ((b * cams + cam) * max_len + q) * s.heads + m;
+  }
+  __device__ __forceinline__ size_t slab(int b, const Shape &s) const {
+    return static_cast<size_t>(b * cams + cam) * s.spatial;
+  }
+  // slot row of (b, q, m) and the factor 1/count, or nullptr outside the grid
+  __device__ __forceinline__ VT *slot(int b, int q, int m, const Shape &s, float &inv) const {
+    const int64_t bev = index[q];
+    if (bev < 0 || bev >= num_query) return nullptr;
+    const int64_t bq = static_cast<int64_t>(b) * num_query + bev;
+    inv = 1.0f / to_float(count[bq]);
+    return slots + (bq * s.heads + m) * s.channels;
+  }
+  template <int C, int CPL>
+  __device__ __forceinline__ void put(int b, int q, int m, int k, const float (&acc)[CPL],
+                                      const Shape &s) const {
+    float inv;
+    VT *row = slot(b, q, m, s, inv);
+    if (row == nullptr) return;
+    float cur[CPL];
+    load16(row + k * CPL, cur);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) cur[c] += acc[c] * inv;
+    store16(row + k * CPL, cur);
+  }
+  __device__ __forceinline__ void put1(int b, int q, int m, int c, float acc,
+                                       const Shape &s) const {
+    float inv;
+    VT *row = slot(b, q, m, s, inv);
+    if (row != nullptr) row[c] = from_float<VT>(to_float(row[c]) + acc * inv);
+  }
+};
+
 // Forward row kernel. Per step (a chunk of NS samples for each lane group),
 // lane i < NG*NS computes one sample's bilinear tap -- the four corner byte
 // offsets (kOobOffset for a corner outside the level) and the four weights
@@ -88,12 +163,13 @@ __device__ __forceinline__ Unit decode_unit(int u, const Shape &s) {
 // in issue order), and every load is unconditional (clamped indices): a load
 // inside a branch is waited for before the branch joins.
 // value_bytes < 2^31 (checked on the host) keeps every offset in 32 bits.
-template <typename VT, typename GT, int C, int NS>
-__global__ void __launch_bounds__(kBlock)
-    msda_forward_rows(const VT *__restrict__ value, uint32_t value_bytes,
-                      const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
-                      const GT *__restrict__ loc, const GT *__restrict__ attn,
-                      VT *__restrict__ out, Shape s, RowPlan plan) {
+template <typename VT, typename GT, int C, int NS, typename Out>
+__device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint32_t value_bytes,
+                                             const int64_t *__restrict__ shapes,
+                                             const int64_t *__restrict__ starts,
+                                             const GT *__restrict__ loc,
+                                             const GT *__restrict__ attn, const Out &out,
+                                             const Shape &s, const RowPlan &plan) {
   constexpr int CPL = RowTraits<VT>::kCpl;
   constexpr int VB = static_cast<int>(sizeof(VT));
   constexpr int KQ = C / CPL;
@@ -144,13 +220,12 @@ __global__ void __launch_bounds__(kBlock)
     const int smp = s0 + tgi + GU * tj;
     ok = live && smp < s.lp;
     sm = ok ? smp : 0;
-    const size_t o = live ? static_cast<size_t>(tu.si(s)) * s.lp + sm : 0;
+    const size_t o = live ? static_cast<size_t>(out.geo_row(tu.b, tu.q, tu.m, s)) * s.lp + sm : 0;
     lx = to_float(loc[2 * o]);
     ly = to_float(loc[2 * o + 1]);
     a = to_float(attn[o]);
-    unit_base = live ? static_cast<uint32_t>(
-                           (static_cast<size_t>(tu.b) * s.spatial * MC + tu.m * C) * VB)
-                     : 0u;
+    unit_base =
+        live ? static_cast<uint32_t>((out.slab(tu.b, s) * MC + tu.m * C) * VB) : 0u;
   };
   load_geometry(0);
   float acc[CPL];
@@ -208,14 +283,34 @@ __global__ void __launch_bounds__(kBlock)
         for (int j = 0; j < CPL; ++j) acc[j] += __shfl_xor(acc[j], off, kWave);
       }
       const int64_t u64 = u_first + static_cast<int64_t>(st / chunks) * UW + slot;
-      if (u64 < s.units && gi == 0) {
-        store16(out + static_cast<size_t>(ou.si(s)) * C + k * CPL, acc);
-      }
+      if (u64 < s.units && gi == 0) out.template put<C, CPL>(ou.b, ou.q, ou.m, k, acc, s);
       ou.advance(UW, s);
 #pragma unroll
       for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
     }
   }
+}
+
+template <typename VT, typename GT, int C, int NS>
+__global__ void __launch_bounds__(kBlock)
+    msda_forward_rows(const VT *__restrict__ value, uint32_t value_bytes,
+                      const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
+                      const GT *__restrict__ loc, const GT *__restrict__ attn,
+                      VT *__restrict__ out, Shape s, RowPlan plan) {
+  forward_rows<VT, GT, C, NS>(value, value_bytes, shapes, starts, loc, attn, DenseRows<VT>{out},
+                              s, plan);
+}
+
+// One camera of the spatial cross-attention, summed into the BEV slots
+// (ScatterAverage above); s.batch, s.queries are the batch and valid_len.
+template <typename VT, typename GT, int C, int NS>
+__global__ void __launch_bounds__(kBlock)
+    msda_forward_scatter_div_rows(const VT *__restrict__ value, uint32_t value_bytes,
+                                  const int64_t *__restrict__ shapes,
+                                  const int64_t *__restrict__ starts, const GT *__restrict__ loc,
+                                  const GT *__restrict__ attn, ScatterAverage<VT, GT> out,
+                                  Shape s, RowPlan plan) {
+  forward_rows<VT, GT, C, NS>(value, value_bytes, shapes, starts, loc, attn, out, s, plan);
 }
 
 // ------------------------------------------------------------ backward ---
@@ -341,11 +436,13 @@ __global__ void __launch_bounds__(kBlock)
 
 // ------------------------------------------------------- generic (any C) ---
 
-template <typename VT, typename GT>
-__global__ void __launch_bounds__(kBlock)
-    msda_forward_generic(const VT *__restrict__ value, const int64_t *__restrict__ shapes,
-                         const int64_t *__restrict__ starts, const GT *__restrict__ loc,
-                         const GT *__restrict__ attn, VT *__restrict__ out, Shape s) {
+template <typename VT, typename GT, typename Out>
+__device__ __forceinline__ void forward_generic(const VT *__restrict__ value,
+                                                const int64_t *__restrict__ shapes,
+                                                const int64_t *__restrict__ starts,
+                                                const GT *__restrict__ loc,
+                                                const GT *__restrict__ attn, const Out &out,
+                                                const Shape &s) {
   __shared__ Level lv[kMaxLevels];
   stage_levels(lv, shapes, starts, s);
   const int C = s.channels, MC = s.heads * C;
@@ -353,12 +450,14 @@ __global__ void __launch_bounds__(kBlock)
   for (int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; idx < total;
        idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int c = static_cast<int>(idx % C);
-    const int si = static_cast<int>(idx / C);
+    const int si = static_cast<int>(idx / C);  // (b*nq + q)*M + m
     const int m = si % s.heads;
+    const int q = (si / s.heads) % s.queries;
     const int b = si / (s.heads * s.queries);
-    const VT *vbase = value + static_cast<size_t>(b) * s.spatial * MC + m * C + c;
-    const GT *lbase = loc + static_cast<size_t>(si) * s.lp * 2;
-    const GT *abase = attn + static_cast<size_t>(si) * s.lp;
+    const int row = out.geo_row(b, q, m, s);
+    const VT *vbase = value + out.slab(b, s) * MC + m * C + c;
+    const GT *lbase = loc + static_cast<size_t>(row) * s.lp * 2;
+    const GT *abase = attn + static_cast<size_t>(row) * s.lp;
     float acc = 0.0f;
     for (int smp = 0; smp < s.lp; ++smp) {
       const Level L = lv[smp / s.points];
@@ -372,7 +471,73 @@ __global__ void __launch_bounds__(kBlock)
       acc += a * (t.wy0 * t.wx0) * v00 + a * (t.wy0 * t.wx1) * v01 +
              a * (t.wy1 * t.wx0) * v10 + a * (t.wy1 * t.wx1) * v11;
     }
-    out[idx] = from_float<VT>(acc);
+    out.put1(b, q, m, c, acc, s);
+  }
+}
+
+template <typename VT, typename GT>
+__global__ void __launch_bounds__(kBlock)
+    msda_forward_generic(const VT *__restrict__ value, const int64_t *__restrict__ shapes,
+                         const int64_t *__restrict__ starts, const GT *__restrict__ loc,
+                         const GT *__restrict__ attn, VT *__restrict__ out, Shape s) {
+  forward_generic<VT, GT>(value, shapes, starts, loc, attn, DenseRows<VT>{out}, s);
+}
+
+template <typename VT, typename GT>
+__global__ void __launch_bounds__(kBlock)
+    msda_forward_scatter_div_generic(const VT *__restrict__ value,
+                                     const int64_t *__restrict__ shapes,
+                                     const int64_t *__restrict__ starts,
+                                     const GT *__restrict__ loc, const GT *__restrict__ attn,
+                                     ScatterAverage<VT, GT> out, Shape s) {
+  forward_generic<VT, GT>(value, shapes, starts, loc, attn, out, s);
+}
+
+// Backward of one camera's scatter-average: the gradient of the camera's MSDA
+// output rows, grad_out[(b*cams + cam)*max_len + r][row] =
+// grad_slots[b, index[r]][row] / count[b, index[r]] for r < valid_len; rows
+// past valid_len (the rebatch padding) and indices outside [0, num_query) get
+// zeros. W = 16 / sizeof(VT) elements per thread (16-byte rows) or 1.
+template <typename VT, typename GT, int W>
+__global__ void __launch_bounds__(kBlock)
+    msda_scatter_div_grad(const VT *__restrict__ grad_slots, const int64_t *__restrict__ index,
+                          const GT *__restrict__ count, VT *__restrict__ grad_out, int batch,
+                          int cams, int cam, int valid_len, int max_len, int num_query,
+                          int row) {
+  static_assert(W == 1 || W * sizeof(VT) == 16, "one element or one 16-byte chunk per thread");
+  const int per_row = row / W;
+  const int64_t total = static_cast<int64_t>(batch) * max_len * per_row;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int j = static_cast<int>(i % per_row);
+    const int64_t br = i / per_row;
+    const int r = static_cast<int>(br % max_len);
+    const int b = static_cast<int>(br / max_len);
+    float v[W];
+#pragma unroll
+    for (int e = 0; e < W; ++e) v[e] = 0.0f;
+    if (r < valid_len) {
+      const int64_t bev = index[r];
+      if (bev >= 0 && bev < num_query) {
+        const int64_t bq = static_cast<int64_t>(b) * num_query + bev;
+        const float inv = 1.0f / to_float(count[bq]);
+        const VT *src = grad_slots + bq * row + static_cast<int64_t>(j) * W;
+        if constexpr (W == 1) {
+          v[0] = to_float(src[0]);
+        } else {
+          load16(src, v);
+        }
+#pragma unroll
+        for (int e = 0; e < W; ++e) v[e] *= inv;
+      }
+    }
+    VT *dst = grad_out + (static_cast<int64_t>(b * cams + cam) * max_len + r) * row +
+              static_cast<int64_t>(j) * W;
+    if constexpr (W == 1) {
+      dst[0] = from_float<VT>(v[0]);
+    } else {
+      store16(dst, v);
+    }
   }
 }
 

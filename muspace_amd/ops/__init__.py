@@ -7,6 +7,7 @@ from .multi_scale_deformable_attn import (
     multi_scale_deformable_attn_pytorch,
     multi_scale_deformable_attn_pytorch_compat,
 )
+from .scatter_div import multi_scale_deformable_attn_scatter_div
 
 __all__ = [
     "explain_dispatch",
@@ -14,4 +15,5 @@ __all__ = [
     "multi_scale_deformable_attn",
     "multi_scale_deformable_attn_pytorch",
     "multi_scale_deformable_attn_pytorch_compat",
+    "multi_scale_deformable_attn_scatter_div",
 ]

@@ -25,7 +25,7 @@ from pathlib import Path
 from typing import Any, Callable
 
 LIBRARY_RELPATH = "native/libmuspace_msda.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
@@ -57,6 +57,16 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         + [_c_ptr, ctypes.c_size_t, _c_ptr],
     ),
     "ms_deform_attn_backward_workspace_size": (ctypes.c_size_t, [_c_int] + [_c_int64] * 7),
+    "ms_deform_attn_forward_scatter_div": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 11
+        + [_c_ptr],
+    ),
+    "ms_deform_attn_scatter_div_grad": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_ptr] + [_c_int64] * 7 + [_c_ptr],
+    ),
 }
 
 
@@ -118,6 +128,8 @@ class NativeLibrary:
         self._bound: dict[str, Callable[..., Any]] = {
             "ms_deform_attn_forward": self.ms_deform_attn_forward,
             "ms_deform_attn_backward": self.ms_deform_attn_backward,
+            "ms_deform_attn_forward_scatter_div": self.ms_deform_attn_forward_scatter_div,
+            "ms_deform_attn_scatter_div_grad": self.ms_deform_attn_scatter_div_grad,
             "add_one": self.add_one,
         }
 
@@ -244,6 +256,91 @@ class NativeLibrary:
                 int(im2col_step), workspace.data_ptr(), int(nbytes), self._stream(value),
             )
         self._raise_on(rc, "ms_deform_attn_backward")
+
+    def ms_deform_attn_forward_scatter_div(
+        self, value, spatial_shapes, level_start_index, sampling_locations,
+        attention_weights, index, count, slots, num_cams: int, cam_id: int,
+    ) -> None:
+        """One camera of the spatial cross-attention, added into ``slots`` in place.
+
+        value ``[bs*num_cams, nv, M, C]``, sampling_locations
+        ``[bs*num_cams, max_len, M, L, P, 2]``, attention_weights
+        ``[bs*num_cams, max_len, M, L, P]``, index ``[valid_len]`` int64 (the BEV
+        query of each of the camera's first valid_len rows), count
+        ``[bs, num_query]`` and slots ``[bs, num_query, M*C]``. Argument order of
+        the reference's ``ms_deformable_im2col_scatter_div_musa``
+        (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:455-505).
+        """
+        import torch
+
+        half = (torch.float32, torch.float16, torch.bfloat16)
+        _check(value, "value", half)
+        _check(spatial_shapes, "spatial_shapes", (torch.int64,))
+        _check(level_start_index, "level_start_index", (torch.int64,))
+        geom = (torch.float32,) if value.dtype == torch.float32 else (torch.float32, value.dtype)
+        _check(sampling_locations, "sampling_locations", geom)
+        _check(attention_weights, "attention_weights", (sampling_locations.dtype,))
+        _check(index, "index", (torch.int64,))
+        _check(count, "count", (sampling_locations.dtype,))
+        _check(slots, "slots", (value.dtype,))
+        if value.dim() != 4 or sampling_locations.dim() != 6 or index.dim() != 1:
+            raise RuntimeError("value must be 4-D, sampling_locations 6-D and index 1-D")
+        if slots.dim() != 3:
+            raise RuntimeError("slots must be 3-D [batch, num_query, num_heads*channels]")
+        rows, spatial, heads, channels = value.shape
+        if num_cams <= 0 or rows % num_cams != 0:
+            raise RuntimeError(f"value rows {rows} are not a multiple of num_cams {num_cams}")
+        batch, num_query = rows // num_cams, slots.shape[1]
+        levels = spatial_shapes.shape[0]
+        max_len, points = sampling_locations.shape[1], sampling_locations.shape[4]
+        valid_len = index.shape[0]
+        _check_shape(spatial_shapes, "spatial_shapes", (levels, 2))
+        _check_shape(level_start_index, "level_start_index", (levels,))
+        _check_shape(sampling_locations, "sampling_locations",
+                     (rows, max_len, heads, levels, points, 2))
+        _check_shape(attention_weights, "attention_weights", (rows, max_len, heads, levels, points))
+        _check_shape(count, "count", (batch, num_query))
+        _check_shape(slots, "slots", (batch, num_query, heads * channels))
+        with torch.cuda.device(value.device):
+            rc = self._raw["ms_deform_attn_forward_scatter_div"](
+                value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
+                level_start_index.data_ptr(), sampling_locations.data_ptr(),
+                attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
+                index.data_ptr(), count.data_ptr(), slots.data_ptr(), batch, num_cams,
+                int(cam_id), valid_len, spatial, heads, channels, levels, max_len, points,
+                num_query, self._stream(value),
+            )
+        self._raise_on(rc, "ms_deform_attn_forward_scatter_div")
+
+    def ms_deform_attn_scatter_div_grad(
+        self, grad_slots, index, count, grad_output, num_cams: int, cam_id: int,
+    ) -> None:
+        """Camera cam_id's rows of grad_output ``[bs*num_cams, max_len, row]`` from
+        grad_slots ``[bs, num_query, row]``: ``grad_slots[b, index[r]] / count[b,
+        index[r]]`` for r < len(index), zero past it."""
+        import torch
+
+        half = (torch.float32, torch.float16, torch.bfloat16)
+        _check(grad_slots, "grad_slots", half)
+        _check(index, "index", (torch.int64,))
+        geom = (torch.float32,) if grad_slots.dtype == torch.float32 else (
+            torch.float32, grad_slots.dtype)
+        _check(count, "count", geom)
+        _check(grad_output, "grad_output", (grad_slots.dtype,))
+        if grad_slots.dim() != 3 or grad_output.dim() != 3 or index.dim() != 1:
+            raise RuntimeError("grad_slots and grad_output must be 3-D and index 1-D")
+        batch, num_query, row = grad_slots.shape
+        rows, max_len = grad_output.shape[0], grad_output.shape[1]
+        _check_shape(grad_output, "grad_output", (batch * num_cams, max_len, row))
+        _check_shape(count, "count", (batch, num_query))
+        with torch.cuda.device(grad_slots.device):
+            rc = self._raw["ms_deform_attn_scatter_div_grad"](
+                grad_slots.data_ptr(), _dtype_code(grad_slots.dtype), index.data_ptr(),
+                count.data_ptr(), _dtype_code(count.dtype), grad_output.data_ptr(), batch,
+                num_cams, int(cam_id), index.shape[0], max_len, num_query, row,
+                self._stream(grad_slots),
+            )
+        self._raise_on(rc, "ms_deform_attn_scatter_div_grad")
 
     def add_one(self, value, actual) -> None:
         """Build smoke: actual = value + 1 (float32 device tensors)."""

@@ -161,3 +161,73 @@ def algorithmic_bytes(
     fwd = n_value * vb + n_loc * gb + n_attn * gb + n_out * vb
     bwd = n_value * vb + n_loc * gb + n_attn * gb + n_out * vb + 4 * (n_value + n_loc + n_attn)
     return fwd, bwd
+
+
+# ------------------------------------------------ spatial cross-attention ---
+
+SCA_BEV = (200, 200)  # BEVFormer-base BEV grid: 40000 queries
+SCA_CAMERAS = 6
+SCA_FOV_DEG = 90.0
+
+
+def sca_camera_indexes(
+    bev_h: int = SCA_BEV[0],
+    bev_w: int = SCA_BEV[1],
+    num_cams: int = SCA_CAMERAS,
+    fov_deg: float = SCA_FOV_DEG,
+) -> tuple[list[torch.Tensor], torch.Tensor]:
+    """(indexes, count) of a synthetic camera ring, on the CPU.
+
+    num_cams cameras sit at the centre of the BEV grid; camera i looks along
+    360*i/num_cams degrees and sees the cells whose centre lies within fov_deg/2
+    of that direction. ``indexes[i]`` lists those cells (row-major BEV ids, in
+    increasing order, as ``nonzero`` gives them) and ``count`` ``[bev_h*bev_w]``
+    is the number of cameras that see each cell, at least 1 (BEVFormer's
+    ``count.clamp(min=1)``). At the defaults each camera sees 9900 or 10000 of
+    the 40000 cells and about half of the cells are seen by two cameras.
+    """
+    ys, xs = torch.meshgrid(torch.arange(bev_h, dtype=torch.float64),
+                            torch.arange(bev_w, dtype=torch.float64), indexing="ij")
+    angle = torch.rad2deg(torch.atan2(ys + 0.5 - bev_h / 2, xs + 0.5 - bev_w / 2)).flatten()
+    indexes = []
+    count = torch.zeros(bev_h * bev_w, dtype=torch.float32)
+    for cam in range(num_cams):
+        off = (angle - 360.0 * cam / num_cams + 180.0) % 360.0 - 180.0
+        seen = off.abs() < fov_deg / 2
+        indexes.append(torch.nonzero(seen).flatten())
+        count += seen.float()
+    return indexes, count.clamp_(min=1.0)
+
+
+def make_sca_inputs(
+    *,
+    seed: int = DEFAULT_SEED,
+    device: str | torch.device = "cpu",
+) -> dict[str, object]:
+    """c2's tensors as one BEVFormer sample's six rebatched cameras, plus the
+    camera ring of :func:`sca_camera_indexes` (max valid rows 10000 = c2's nq)."""
+    cfg = CONFIGS["c2"]
+    assert cfg.batch == SCA_CAMERAS
+    inputs = make_inputs(cfg, seed=seed, device=device, with_grad_output=False)
+    indexes, count = sca_camera_indexes()
+    assert max(len(i) for i in indexes) <= cfg.queries
+    inputs["indexes"] = [i.to(device) for i in indexes]
+    inputs["count"] = count.view(1, -1).to(device)
+    return inputs
+
+
+def sca_algorithmic_bytes(valid_rows: int, cameras: int, num_query: int,
+                          cfg: MSDAConfig | None = None) -> int:
+    """Algorithmic bytes of the fused scatter-average forward (fp32).
+
+    Every tensor once at its storage width: the cameras' value, the geometry
+    of the valid rows (loc, attn), their int64 index and float32 count
+    entries, and the slots read once and written once. Padding rows are not
+    read.
+    """
+    cfg = cfg or CONFIGS["c2"]
+    n_value = cfg.batch * cfg.spatial_size * cfg.heads * cfg.channels
+    per_row = cfg.heads * cfg.num_levels * cfg.points  # attention weights per row
+    row = cfg.heads * cfg.channels
+    slots = (cfg.batch // cameras) * num_query * row
+    return 4 * n_value + valid_rows * (4 * 3 * per_row + 8 + 4) + 2 * 4 * slots

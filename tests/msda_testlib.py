@@ -90,3 +90,51 @@ def max_violation(actual, expected, rtol: float, atol: float) -> float:
     if a.size == 0:
         return -1.0
     return float(np.max(np.abs(a - e) - atol - rtol * np.abs(e)))
+
+
+def scatter_div_case(
+    seed: int,
+    *,
+    batch=2,
+    cams=3,
+    max_len=9,
+    num_query=20,
+    heads=2,
+    channels=4,
+    levels=((3, 5), (2, 2)),
+    points=3,
+    lengths=None,
+    out_of_range=False,
+    dtype=torch.float64,
+):
+    """Camera-rebatched inputs of the fused scatter-average.
+
+    Returns (value, shapes, starts, loc, attn, indexes, count, slots): value
+    ``[batch*cams, nv, M, C]``, geometry ``[batch*cams, max_len, ...]``, one
+    index tensor per camera (distinct BEV ids; ``lengths`` fixes how many),
+    count ``[batch, num_query]`` = (b + 1) x cameras seeing each query (at
+    least 1) and random initial slots.
+    Default lengths: max_len for camera 0, 0 for camera 1 (an empty camera),
+    random below max_len for the rest. ``out_of_range`` appends ids -1 and
+    num_query to the last camera.
+    """
+    g = torch.Generator().manual_seed(seed)
+    rows = batch * cams
+    value, shapes, starts, loc, attn, _ = random_case(
+        seed, batch=rows, queries=max_len, heads=heads, channels=channels, levels=levels,
+        points=points, dtype=dtype)
+    if lengths is None:
+        lengths = [max_len, 0] + [
+            int(torch.randint(1, max_len, (1,), generator=g)) for _ in range(cams - 2)]
+    indexes = []
+    seen = torch.zeros(num_query, dtype=dtype)
+    for cam in range(cams):
+        ids = torch.randperm(num_query, generator=g)[: lengths[cam]]
+        seen[ids] += 1
+        if out_of_range and cam == cams - 1:
+            ids = torch.cat([ids, torch.tensor([-1, num_query])])[:max_len]
+        indexes.append(ids.to(torch.int64))
+    # cameras seeing each query, scaled by b + 1 so that batch entries differ
+    count = torch.stack([seen.clamp(min=1) * (b + 1) for b in range(batch)])
+    slots = torch.randn(batch, num_query, heads * channels, generator=g, dtype=dtype)
+    return value, shapes, starts, loc, attn, indexes, count, slots

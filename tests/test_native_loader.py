@@ -84,7 +84,7 @@ def test_nonzero_return_code_becomes_runtime_error(monkeypatch, tmp_path):
     )
     _build_fake_library(
         tmp_path,
-        "int muspace_abi_version(void) { return 1; }\n"
+        f"int muspace_abi_version(void) {{ return {native.ABI_VERSION}; }}\n"
         'const char *muspace_last_error(void) { return "simulated: batch is not divisible"; }\n'
         + stubs + "\n",
     )

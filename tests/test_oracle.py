@@ -341,3 +341,80 @@ def test_float32_oracle_uses_grid_sample_fma_coordinate():
         dtype=np.float32,
     )
     assert np.array_equal(out.numpy(), expect)
+
+
+# ------------------------------------- spatial cross-attention scatter-average ---
+
+def _scatter_div_inputs(seed, **kw):
+    from msda_testlib import scatter_div_case
+
+    return scatter_div_case(seed, **kw)
+
+
+def _direct_scatter_div(value, shapes, loc, attn, indexes, count, slots):
+    from oracle import msda_scatter_div
+
+    return msda_scatter_div.scatter_div_direct(
+        value.numpy(), shapes.numpy(), loc.numpy(), attn.numpy(),
+        [i.numpy() for i in indexes], count.numpy(), slots.numpy())
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_scatter_div_matches_direct_loops(seed):
+    """Two formulations: per-camera scaled adds on grid_sample vs float64 loops
+    that sum a slot's cameras first and divide once."""
+    from oracle import msda_scatter_div
+
+    value, shapes, _, loc, attn, indexes, count, slots = _scatter_div_inputs(
+        seed, out_of_range=seed == 2)
+    actual = msda_scatter_div.scatter_div(value, shapes, loc, attn, indexes, count, slots)
+    expected = _direct_scatter_div(value, shapes, loc, attn, indexes, count, slots)
+    np.testing.assert_allclose(actual.numpy(), expected, rtol=1e-12, atol=1e-12)
+
+
+def test_scatter_div_constant_value_gives_unit_average():
+    """value = 1 and every corner inside its level: each camera's MSDA row is
+    sum(attn) = 1, so a slot seen by k cameras gets k * (1 / k) = 1 (count here
+    is the plain camera count) and an unseen slot keeps its value (0)."""
+    from oracle import msda_scatter_div
+
+    levels = ((4, 6), (3, 3))
+    value, shapes, _, loc, attn, indexes, _, slots = _scatter_div_inputs(4, levels=levels)
+    value = torch.ones_like(value)
+    for level, (h, w) in enumerate(levels):  # x = loc*W - 0.5 strictly inside [0, W-1]
+        loc[..., level, :, 0] = 0.6 / w + loc[..., level, :, 0].clamp(0, 1) * (1 - 1.2 / w)
+        loc[..., level, :, 1] = 0.6 / h + loc[..., level, :, 1].clamp(0, 1) * (1 - 1.2 / h)
+    seen = torch.zeros(slots.shape[1], dtype=torch.float64)
+    for index in indexes:
+        seen[index] += 1
+    count = seen.clamp(min=1).expand(slots.shape[0], -1).contiguous()
+    result = msda_scatter_div.scatter_div(value, shapes, loc, attn, indexes, count,
+                                          torch.zeros_like(slots))
+    expected = (seen > 0).to(torch.float64).view(1, -1, 1).expand_as(result)
+    np.testing.assert_allclose(result.numpy(), expected.numpy(), rtol=0, atol=1e-12)
+
+
+def test_scatter_div_direct_check_catches_a_camera_major_row_order():
+    """Planted mistake: rows read as cam*batch + b instead of b*cams + cam."""
+    from oracle import msda_scatter_div
+
+    batch, cams = 2, 3
+    value, shapes, _, loc, attn, indexes, count, slots = _scatter_div_inputs(
+        5, batch=batch, cams=cams, lengths=[9, 6, 4])
+    perm = torch.tensor([cam * batch + b for b in range(batch) for cam in range(cams)])
+    mutant = msda_scatter_div.scatter_div(value[perm], shapes, loc[perm], attn[perm], indexes,
+                                          count, slots)
+    expected = _direct_scatter_div(value, shapes, loc, attn, indexes, count, slots)
+    assert not np.allclose(mutant.numpy(), expected, rtol=1e-6, atol=1e-6)
+
+
+def test_scatter_div_gradcheck():
+    from oracle import msda_scatter_div
+
+    value, shapes, _, loc, attn, indexes, count, slots = _scatter_div_inputs(
+        6, batch=1, cams=2, max_len=4, num_query=6, heads=1, channels=2,
+        levels=((2, 3),), points=2, lengths=[4, 3])
+    args = [t.clone().requires_grad_(True) for t in (value, loc, attn, slots)]
+    assert torch.autograd.gradcheck(
+        lambda v, l, a, s: msda_scatter_div.scatter_div(v, shapes, l, a, indexes, count, s),
+        args, eps=1e-6, atol=1e-6)
