@@ -39,7 +39,14 @@ if str(ROOT) not in sys.path:
 
 import torch  # noqa: E402
 
-from muspace_amd.workloads import CONFIGS, HBM_PEAK_GBPS, algorithmic_bytes, make_inputs  # noqa: E402
+from muspace_amd.workloads import (  # noqa: E402
+    CONFIGS,
+    HBM_PEAK_GBPS,
+    algorithmic_bytes,
+    make_inputs,
+    make_sca_inputs,
+    sca_algorithmic_bytes,
+)
 
 METRIC = "MSDA fwd+bwd µs/call + effective GB/s (% HBM peak), BEVFormer SCA shape"
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_c2_fp32.json"
@@ -122,6 +129,101 @@ def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True) -> 
     return res
 
 
+def _event_ms(fn, steps: int, warmup: int) -> float:
+    """Mean ms of fn() over `steps` calls, HIP events on the current stream."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_sca(lib, steps: int = 50, warmup: int = 10) -> dict:
+    """BEVFormer spatial cross-attention epilogue at c2 (one sample, six cameras,
+    200 x 200 BEV grid): the fused scatter-average against the unfused
+    composition (dense MSDA output, per-camera ``slots[idx] += out``, then
+    ``slots / count``), forward and forward + backward."""
+    from muspace_amd import multi_scale_deformable_attn, multi_scale_deformable_attn_scatter_div
+
+    t = make_sca_inputs(device="cuda")
+    value, shapes, starts = t["value"], t["spatial_shapes"], t["level_start_index"]
+    loc, attn, indexes, count = (t["sampling_locations"], t["attention_weights"], t["indexes"],
+                                 t["count"])
+    cams, max_len = len(indexes), loc.shape[1]
+    row = value.shape[2] * value.shape[3]
+    slots = torch.zeros((1, count.shape[1], row), device="cuda")
+
+    index_all = torch.cat(indexes)
+    lens = [int(i.numel()) for i in indexes]
+
+    def fused_kernels():  # the all-camera launch alone
+        lib.ms_deform_attn_forward_scatter_div_cams(value, shapes, starts, loc, attn, index_all,
+                                                    lens, count, slots)
+
+    def per_camera_kernels():  # the reference's interface: one ordered launch per camera
+        for cam, index in enumerate(indexes):
+            lib.ms_deform_attn_forward_scatter_div(value, shapes, starts, loc, attn, index, count,
+                                                   slots, cams, cam)
+
+    def fused():
+        return multi_scale_deformable_attn_scatter_div(value, shapes, starts, loc, attn, indexes,
+                                                       count)
+
+    def unfused():
+        out = multi_scale_deformable_attn(value, shapes, starts, loc, attn).view(
+            1, cams, max_len, row)
+        acc = torch.zeros((1, count.shape[1], row), device="cuda")
+        for cam, index in enumerate(indexes):
+            acc[:, index] += out[:, cam, : len(index)]
+        return acc / count[..., None]
+
+    grad = torch.randn((1, count.shape[1], row), generator=torch.Generator().manual_seed(1))
+    grad = grad.to("cuda")
+    leaves = [x.detach().requires_grad_(True) for x in (value, loc, attn)]
+
+    def train(fn):
+        def step():
+            v, l, a = leaves
+            for x in leaves:
+                x.grad = None
+            if fn is fused:
+                y = multi_scale_deformable_attn_scatter_div(v, shapes, starts, l, a, indexes, count)
+            else:
+                out = multi_scale_deformable_attn(v, shapes, starts, l, a).view(
+                    1, cams, max_len, row)
+                y = torch.zeros((1, count.shape[1], row), device="cuda")
+                for cam, index in enumerate(indexes):
+                    y[:, index] += out[:, cam, : len(index)]
+                y = y / count[..., None]
+            y.backward(grad)
+        return step
+
+    kernel_ms = _event_ms(fused_kernels, steps, warmup)
+    valid = sum(int(i.numel()) for i in indexes)
+    nbytes = sca_algorithmic_bytes(valid, cams, count.shape[1])
+    res = {
+        "workload": f"c2 as 1 sample x {cams} cameras, BEV 200x200 = {count.shape[1]} queries, "
+                    f"{valid} valid camera rows (max_len {max_len})",
+        "fused_kernels_us": round(kernel_ms * 1e3, 1),
+        "per_camera_kernels_us": round(_event_ms(per_camera_kernels, steps, warmup) * 1e3, 1),
+        "fused_fwd_us": round(_event_ms(fused, steps, warmup) * 1e3, 1),
+        "unfused_fwd_us": round(_event_ms(unfused, steps, warmup) * 1e3, 1),
+        "fused_fwd_bwd_us": round(_event_ms(train(fused), steps // 2, warmup) * 1e3, 1),
+        "unfused_fwd_bwd_us": round(_event_ms(train(unfused), steps // 2, warmup) * 1e3, 1),
+        "algorithmic_bytes": nbytes,
+        "effective_GBps": round(nbytes / (kernel_ms * 1e-3) / 1e9, 1),
+    }
+    res["pct_hbm_peak"] = round(100 * res["effective_GBps"] / HBM_PEAK_GBPS, 2)
+    return res
+
+
 def cpu_baseline(cfg, queries: int) -> dict:
     """The oracle (CPU restatement of the reference's PyTorch path) on a query subset."""
     from oracle import msda_torch
@@ -175,6 +277,8 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extra-configs", action="store_true")
     parser.add_argument("--cpu-queries", type=int, default=500)
+    parser.add_argument("--sca-only", action="store_true",
+                        help="only the fused spatial cross-attention scatter-average leg")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="only run a device-to-device copy of this many MiB, 5 times "
                              "(calibrates the FETCH_SIZE / WRITE_SIZE counters), then exit")
@@ -202,6 +306,9 @@ def main() -> int:
     from muspace_amd.runtime.native import load_native_module
 
     lib = load_native_module()
+    if args.sca_only:
+        print(json.dumps({"sca-scatter-div-float32": time_sca(lib, args.steps, args.warmup)}))
+        return 0
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
     print(f"[bench] inputs for {cfg.name}", file=sys.stderr, flush=True)
@@ -232,6 +339,9 @@ def main() -> int:
             del s
             torch.cuda.empty_cache()
         extra["bevformer-1l-published_ms"] = {"MTT S5000": 4.2387, "A100 (mmcv CUDA)": 4.0895}
+        print("[bench] extra sca-scatter-div", file=sys.stderr, flush=True)
+        extra["sca-scatter-div-float32"] = time_sca(lib)
+        torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu_baseline:

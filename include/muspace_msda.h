@@ -148,19 +148,41 @@ MUSPACE_API int ms_deform_attn_forward_scatter_div(
     int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
     int64_t max_len, int64_t num_point, int64_t num_query, void *stream);
 
-/* Gradient of ms_deform_attn_forward_scatter_div's MSDA output rows for one
- * camera: grad_output[b*num_cams + cam_id, r, :] = grad_slots[b, index[r], :] /
- * count[b, index[r]] for r < valid_len, zero for valid_len <= r < max_len and
- * for skipped indices. grad_slots [batch, num_query, row] and grad_output
+/* All cameras of ms_deform_attn_forward_scatter_div in one call: the same sum
+ * for cameras 0 .. num_cams-1, where camera c's valid_lens[c] rows take their
+ * BEV queries from the concatenated
+ *   index               [sum(valid_lens)] int64 (camera 0's entries, then
+ *                       camera 1's, ...; distinct within a camera)
+ * and valid_lens is a HOST array [num_cams]. float32 slots: up to 16 cameras
+ * per launch, added with fp32 global atomics (the order in which two cameras
+ * reach one slot is not fixed; from zero-initialised slots a sum of two is
+ * exact either way). 16-bit slots: one launch per camera, in order. No
+ * reference counterpart (the reference's sketch launches per camera); same
+ * result as calling ms_deform_attn_forward_scatter_div for each camera in
+ * order. */
+MUSPACE_API int ms_deform_attn_forward_scatter_div_cams(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_weights, int geometry_dtype, const int64_t *index,
+    const int64_t *valid_lens, const void *count, void *slots, int64_t batch, int64_t num_cams,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t max_len, int64_t num_point, int64_t num_query, void *stream);
+
+/* Gradient of the cameras' MSDA output rows under the scatter-average:
+ * grad_output[b*num_cams + c, r, :] = grad_slots[b, q, :] / count[b, q] with
+ * q = the BEV query of camera c's row r (concatenated index and host
+ * valid_lens as in ms_deform_attn_forward_scatter_div_cams) for
+ * r < valid_lens[c], zero for valid_lens[c] <= r < max_len and for skipped
+ * indices. grad_slots [batch, num_query, row] and grad_output
  * [batch*num_cams, max_len, row] are value_dtype; count is float32 or
  * value_dtype. ms_deform_attn_backward on grad_output then gives the value,
  * location and weight gradients. No reference counterpart (the reference's
  * fused path is forward-only); it is the chain rule of the same sum. */
 MUSPACE_API int ms_deform_attn_scatter_div_grad(const void *grad_slots, int value_dtype,
-                                                const int64_t *index, const void *count,
-                                                int count_dtype, void *grad_output,
-                                                int64_t batch, int64_t num_cams, int64_t cam_id,
-                                                int64_t valid_len, int64_t max_len,
+                                                const int64_t *index, const int64_t *valid_lens,
+                                                const void *count, int count_dtype,
+                                                void *grad_output, int64_t batch,
+                                                int64_t num_cams, int64_t max_len,
                                                 int64_t num_query, int64_t row, void *stream);
 
 /* Build smoke: y[i] = x[i] + 1 for i < n (float32). Mirrors add_one

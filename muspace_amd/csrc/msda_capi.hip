@@ -256,40 +256,53 @@ void launch_forward(const void *value, const int64_t *shapes, const int64_t *sta
 // ------------------------------------------ spatial cross-attention epilogue ---
 
 // Camera-rebatched dims of the scatter-average entry points.
-struct CamArgs {
-  int64_t batch, cams, cam, valid_len, max_len, num_query;
+struct CamDims {
+  int64_t batch, cams, max_len, num_query;
 };
 
-// Validates the fused scatter-average call and fills `s` for one camera:
-// s.batch = batch, s.queries = valid_len (the units this launch computes).
-// `full` describes the whole rebatched value and geometry.
-int validate_cameras(const char *fn, const Args &a, const CamArgs &c, int value_dtype,
-                     int geometry_dtype, msda::Shape &s, msda::Shape &full) {
-  if (c.batch < 0 || c.cams <= 0 || c.cam < 0 || c.cam >= c.cams || c.max_len < 0 ||
-      c.valid_len < 0 || c.valid_len > c.max_len || c.num_query < 0) {
+// Checks the camera dims and the dense geometry they imply; `full` describes
+// the whole rebatched value and geometry ([batch*cams, ...]).
+int validate_cameras(const char *fn, const Args &a, const CamDims &c, int value_dtype,
+                     int geometry_dtype, msda::Shape &full) {
+  if (c.batch < 0 || c.cams <= 0 || c.max_len < 0 || c.num_query < 0) {
     return fail(MUSPACE_EINVAL,
-                "%s: invalid dims batch=%lld num_cams=%lld cam_id=%lld valid_len=%lld "
-                "max_len=%lld num_query=%lld (need 0 <= cam_id < num_cams and "
-                "0 <= valid_len <= max_len)",
-                fn, (long long)c.batch, (long long)c.cams, (long long)c.cam,
-                (long long)c.valid_len, (long long)c.max_len, (long long)c.num_query);
+                "%s: invalid dims batch=%lld num_cams=%lld max_len=%lld num_query=%lld", fn,
+                (long long)c.batch, (long long)c.cams, (long long)c.max_len,
+                (long long)c.num_query);
   }
-  if (c.batch * c.cams > INT_MAX) {
-    return fail(MUSPACE_ERANGE, "%s: batch*num_cams exceeds int32", fn);
+  if (c.batch * c.cams > INT_MAX || c.num_query > INT_MAX) {
+    return fail(MUSPACE_ERANGE, "%s: batch*num_cams or num_query exceeds int32", fn);
   }
-  if (int rc = validate(fn, a, value_dtype, geometry_dtype, full)) return rc;
-  s = full;
-  s.batch = static_cast<int>(c.batch);
-  s.queries = static_cast<int>(c.valid_len);
-  s.units = static_cast<int>(c.batch * c.valid_len * a.heads);
+  return validate(fn, a, value_dtype, geometry_dtype, full);
+}
+
+// Checks 0 <= valid_lens[i] <= max_len (host array) and sums them.
+int check_lengths(const char *fn, const int64_t *valid_lens, int64_t cams, int64_t max_len,
+                  int64_t &total) {
+  if (!valid_lens) return fail(MUSPACE_EINVAL, "%s: null valid_lens", fn);
+  total = 0;
+  for (int64_t i = 0; i < cams; ++i) {
+    if (valid_lens[i] < 0 || valid_lens[i] > max_len) {
+      return fail(MUSPACE_EINVAL, "%s: valid_lens[%lld] = %lld is outside [0, max_len=%lld]", fn,
+                  (long long)i, (long long)valid_lens[i], (long long)max_len);
+    }
+    total += valid_lens[i];
+  }
   return ok();
 }
 
-template <typename VT, typename GT>
+// One launch of cameras out.cam0 .. out.cam0 + out.ncam - 1 (out.off[out.ncam]
+// valid rows); `full` is the whole rebatched value.
+template <typename VT, typename GT, bool kAtomic>
 void launch_scatter_div(const void *value, const int64_t *shapes, const int64_t *starts,
-                        const void *loc, const void *attn, const msda::ScatterAverage<VT, GT> &out,
-                        const msda::Shape &s, const msda::Shape &full, void *slots,
-                        hipStream_t st) {
+                        const void *loc, const void *attn,
+                        const msda::CameraSlots<VT, GT, kAtomic> &out, const msda::Shape &full,
+                        int batch, void *slots, hipStream_t st) {
+  msda::Shape s = full;
+  s.batch = batch;
+  s.queries = out.off[out.ncam];
+  s.units = batch * s.queries * s.heads;
+  if (s.units == 0) return;
   const VT *v = static_cast<const VT *>(value);
   const GT *lc = static_cast<const GT *>(loc);
   const GT *aw = static_cast<const GT *>(attn);
@@ -300,9 +313,24 @@ void launch_scatter_div(const void *value, const int64_t *shapes, const int64_t 
   const uint32_t vbytes = static_cast<uint32_t>(vb);
   auto go = [&](auto cc) {
     constexpr int C = decltype(cc)::value;
+    constexpr int KQ = C / msda::RowTraits<VT>::kCpl;
     forward_rows_ns<VT, C>(s, [&](auto ns, const Launch &L) {
-      msda::msda_forward_scatter_div_rows<VT, GT, C, decltype(ns)::value>
-          <<<L.blocks, msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw, out, s, L.plan);
+      // one segment of whole blocks per camera (the plan depends on L*P only)
+      msda::CameraSlots<VT, GT, kAtomic> seg = out;
+      const int64_t per_wave = static_cast<int64_t>((msda::kWave / KQ) >> L.plan.gu_log2) *
+                               L.plan.iters;
+      const int64_t per_block = per_wave * (msda::kBlock / msda::kWave);
+      int64_t blocks = 0;
+      for (int j = 0; j < seg.ncam; ++j) {
+        seg.blk[j] = static_cast<int>(blocks);
+        const int64_t units = static_cast<int64_t>(s.batch) * s.heads *
+                              (seg.off[j + 1] - seg.off[j]);
+        blocks += (units + per_block - 1) / per_block;
+      }
+      seg.blk[seg.ncam] = static_cast<int>(blocks);
+      msda::msda_forward_scatter_div_rows<VT, GT, C, decltype(ns)::value, kAtomic>
+          <<<static_cast<int>(blocks), msda::kBlock, 0, st>>>(v, vbytes, shapes, starts, lc, aw,
+                                                              seg, s, L.plan);
     });
   };
   switch (rows) {
@@ -310,16 +338,29 @@ void launch_scatter_div(const void *value, const int64_t *shapes, const int64_t 
     case 32: go(std::integral_constant<int, 32>()); return;
     case 64: go(std::integral_constant<int, 64>()); return;
     default:
-      msda::msda_forward_scatter_div_generic<VT, GT>
+      msda::msda_forward_scatter_div_generic<VT, GT, kAtomic>
           <<<generic_blocks(static_cast<int64_t>(s.units) * s.channels), msda::kBlock, 0, st>>>(
               v, shapes, starts, lc, aw, out, s);
       return;
   }
 }
 
+// Cameras [cam0, cam0 + ncam) of `valid_lens`, numbered back to back from
+// index + first; returns the camera table of one launch.
+template <typename Table>
+void fill_camera_table(Table &tb, const int64_t *valid_lens, int cam0, int ncam) {
+  int q = 0;
+  for (int j = 0; j < ncam; ++j) {
+    tb.off[j] = q;
+    q += static_cast<int>(valid_lens[cam0 + j]);
+  }
+  tb.off[ncam] = q;
+}
+
 template <typename VT, typename GT>
-void launch_scatter_div_grad(const void *grad_slots, const int64_t *index, const void *count,
-                             void *grad_out, const CamArgs &c, int row, hipStream_t st) {
+void launch_scatter_div_grad(const void *grad_slots, const int64_t *index,
+                             const int64_t *valid_lens, const void *count, void *grad_out,
+                             const CamDims &c, int row, hipStream_t st) {
   constexpr int W = 16 / static_cast<int>(sizeof(VT));
   const VT *g = static_cast<const VT *>(grad_slots);
   const GT *cnt = static_cast<const GT *>(count);
@@ -327,14 +368,26 @@ void launch_scatter_div_grad(const void *grad_slots, const int64_t *index, const
   const bool vec = row % W == 0 && aligned(grad_slots, 16) && aligned(grad_out, 16);
   const int64_t work = c.batch * c.max_len * (vec ? row / W : row);
   const int B = static_cast<int>(c.batch), NC = static_cast<int>(c.cams),
-            cam = static_cast<int>(c.cam), V = static_cast<int>(c.valid_len),
             ML = static_cast<int>(c.max_len), NQ = static_cast<int>(c.num_query);
-  if (vec) {
-    msda::msda_scatter_div_grad<VT, GT, W><<<generic_blocks(work), msda::kBlock, 0, st>>>(
-        g, index, cnt, o, B, NC, cam, V, ML, NQ, row);
-  } else {
-    msda::msda_scatter_div_grad<VT, GT, 1><<<generic_blocks(work), msda::kBlock, 0, st>>>(
-        g, index, cnt, o, B, NC, cam, V, ML, NQ, row);
+  int64_t first = 0;
+  for (int cam0 = 0; cam0 < NC; cam0 += msda::kMaxCams) {
+    const int ncam = NC - cam0 < msda::kMaxCams ? NC - cam0 : msda::kMaxCams;
+    msda::CameraRows tb{};
+    int q = 0;
+    for (int j = 0; j < ncam; ++j) {
+      tb.off[j] = q;
+      tb.len[j] = static_cast<int>(valid_lens[cam0 + j]);
+      q += tb.len[j];
+    }
+    const dim3 grid(generic_blocks(work), ncam);
+    if (vec) {
+      msda::msda_scatter_div_grad<VT, GT, W><<<grid, msda::kBlock, 0, st>>>(
+          g, index + first, cnt, o, B, NC, cam0, tb, ML, NQ, row);
+    } else {
+      msda::msda_scatter_div_grad<VT, GT, 1><<<grid, msda::kBlock, 0, st>>>(
+          g, index + first, cnt, o, B, NC, cam0, tb, ML, NQ, row);
+    }
+    first += q;
   }
 }
 
@@ -740,32 +793,113 @@ int ms_deform_attn_forward_scatter_div(
   const int64_t rows = batch * num_cams;
   const Args a{rows, spatial_size, num_heads, channels, num_levels, max_len, num_point,
                rows > 0 ? rows : 1};
-  const CamArgs c{batch, num_cams, cam_id, valid_len, max_len, num_query};
-  msda::Shape s, full;
-  if (int rc = validate_cameras(fn, a, c, value_dtype, geometry_dtype, s, full)) return rc;
-  if (!needs_data(s) || s.lp == 0) return ok();  // nothing is added to the slots
+  const CamDims c{batch, num_cams, max_len, num_query};
+  msda::Shape full;
+  if (int rc = validate_cameras(fn, a, c, value_dtype, geometry_dtype, full)) return rc;
+  if (cam_id < 0 || cam_id >= num_cams || valid_len < 0 || valid_len > max_len) {
+    return fail(MUSPACE_EINVAL,
+                "%s: need 0 <= cam_id < num_cams and 0 <= valid_len <= max_len (cam_id=%lld "
+                "num_cams=%lld valid_len=%lld max_len=%lld)",
+                fn, (long long)cam_id, (long long)num_cams, (long long)valid_len,
+                (long long)max_len);
+  }
+  // nothing is added (with num_query == 0 every index is skipped)
+  if (batch == 0 || valid_len == 0 || full.lp == 0 || num_query == 0) return ok();
   if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
       !attention_weights || !index || !count || !slots) {
     return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
   }
-  const int cams = static_cast<int>(num_cams), cam = static_cast<int>(cam_id),
-            ml = static_cast<int>(max_len), nq = static_cast<int>(num_query);
   hipStream_t st = static_cast<hipStream_t>(stream);
   with_dtypes(value_dtype, geometry_dtype, [&](auto vt, auto gt) {
     using VT = decltype(vt);
     using GT = decltype(gt);
-    const msda::ScatterAverage<VT, GT> out{static_cast<VT *>(slots), index,
-                                           static_cast<const GT *>(count), cams, cam, ml, nq};
-    launch_scatter_div<VT, GT>(value, spatial_shapes, level_start_index, sampling_locations,
-                               attention_weights, out, s, full, slots, st);
+    msda::CameraSlots<VT, GT, false> out{};
+    out.slots = static_cast<VT *>(slots);
+    out.index = index;
+    out.count = static_cast<const GT *>(count);
+    out.cams = static_cast<int>(num_cams);
+    out.cam0 = static_cast<int>(cam_id);
+    out.ncam = 1;
+    out.max_len = static_cast<int>(max_len);
+    out.num_query = static_cast<int>(num_query);
+    out.off[0] = 0;
+    out.off[1] = static_cast<int>(valid_len);
+    launch_scatter_div<VT, GT, false>(value, spatial_shapes, level_start_index,
+                                      sampling_locations, attention_weights, out, full,
+                                      static_cast<int>(batch), slots, st);
+  });
+  return check_launch(fn);
+}
+
+int ms_deform_attn_forward_scatter_div_cams(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_weights, int geometry_dtype, const int64_t *index,
+    const int64_t *valid_lens, const void *count, void *slots, int64_t batch, int64_t num_cams,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t max_len, int64_t num_point, int64_t num_query, void *stream) {
+  static const char *fn = "ms_deform_attn_forward_scatter_div_cams";
+  const int64_t rows = batch * num_cams;
+  const Args a{rows, spatial_size, num_heads, channels, num_levels, max_len, num_point,
+               rows > 0 ? rows : 1};
+  const CamDims c{batch, num_cams, max_len, num_query};
+  msda::Shape full;
+  if (int rc = validate_cameras(fn, a, c, value_dtype, geometry_dtype, full)) return rc;
+  int64_t total = 0;
+  if (int rc = check_lengths(fn, valid_lens, num_cams, max_len, total)) return rc;
+  // nothing is added (with num_query == 0 every index is skipped)
+  if (batch == 0 || total == 0 || full.lp == 0 || num_query == 0) return ok();
+  if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+      !attention_weights || !index || !count || !slots) {
+    return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int cams = static_cast<int>(num_cams);
+  with_dtypes(value_dtype, geometry_dtype, [&](auto vt, auto gt) {
+    using VT = decltype(vt);
+    using GT = decltype(gt);
+    auto fill = [&](auto &out, int cam0, int ncam) {
+      out.slots = static_cast<VT *>(slots);
+      out.count = static_cast<const GT *>(count);
+      out.cams = cams;
+      out.cam0 = cam0;
+      out.ncam = ncam;
+      out.max_len = static_cast<int>(max_len);
+      out.num_query = static_cast<int>(num_query);
+      fill_camera_table(out, valid_lens, cam0, ncam);
+    };
+    int64_t first = 0;  // index entry of the launch's first row
+    if constexpr (std::is_same<VT, float>::value) {
+      // float32 slots: up to kMaxCams cameras per launch, added with atomics
+      for (int cam0 = 0; cam0 < cams; cam0 += msda::kMaxCams) {
+        msda::CameraSlots<float, GT, true> out{};
+        fill(out, cam0, cams - cam0 < msda::kMaxCams ? cams - cam0 : msda::kMaxCams);
+        out.index = index + first;
+        launch_scatter_div<float, GT, true>(value, spatial_shapes, level_start_index,
+                                            sampling_locations, attention_weights, out, full,
+                                            static_cast<int>(batch), slots, st);
+        first += out.off[out.ncam];
+      }
+    } else {
+      // 16-bit slots: one camera per launch, in order, plain read-modify-write
+      for (int cam = 0; cam < cams; ++cam) {
+        msda::CameraSlots<VT, GT, false> out{};
+        fill(out, cam, 1);
+        out.index = index + first;
+        launch_scatter_div<VT, GT, false>(value, spatial_shapes, level_start_index,
+                                          sampling_locations, attention_weights, out, full,
+                                          static_cast<int>(batch), slots, st);
+        first += out.off[1];
+      }
+    }
   });
   return check_launch(fn);
 }
 
 int ms_deform_attn_scatter_div_grad(const void *grad_slots, int value_dtype,
-                                    const int64_t *index, const void *count, int count_dtype,
-                                    void *grad_output, int64_t batch, int64_t num_cams,
-                                    int64_t cam_id, int64_t valid_len, int64_t max_len,
+                                    const int64_t *index, const int64_t *valid_lens,
+                                    const void *count, int count_dtype, void *grad_output,
+                                    int64_t batch, int64_t num_cams, int64_t max_len,
                                     int64_t num_query, int64_t row, void *stream) {
   static const char *fn = "ms_deform_attn_scatter_div_grad";
   if (value_dtype != MUSPACE_DTYPE_F32 && value_dtype != MUSPACE_DTYPE_F16 &&
@@ -777,26 +911,27 @@ int ms_deform_attn_scatter_div_grad(const void *grad_slots, int value_dtype,
     return fail(MUSPACE_EINVAL, "%s: count must be float32 or %s, got %s", fn,
                 dtype_name(value_dtype), dtype_name(count_dtype));
   }
-  const CamArgs c{batch, num_cams, cam_id, valid_len, max_len, num_query};
-  if (batch < 0 || num_cams <= 0 || cam_id < 0 || cam_id >= num_cams || max_len < 0 ||
-      valid_len < 0 || valid_len > max_len || num_query < 0 || row <= 0) {
+  if (batch < 0 || num_cams <= 0 || max_len < 0 || num_query < 0 || row <= 0) {
     return fail(MUSPACE_EINVAL,
-                "%s: invalid dims batch=%lld num_cams=%lld cam_id=%lld valid_len=%lld "
-                "max_len=%lld num_query=%lld row=%lld",
-                fn, (long long)batch, (long long)num_cams, (long long)cam_id,
-                (long long)valid_len, (long long)max_len, (long long)num_query, (long long)row);
+                "%s: invalid dims batch=%lld num_cams=%lld max_len=%lld num_query=%lld row=%lld",
+                fn, (long long)batch, (long long)num_cams, (long long)max_len,
+                (long long)num_query, (long long)row);
   }
   if (batch * num_cams > INT_MAX || max_len > INT_MAX || num_query > INT_MAX || row > INT_MAX) {
     return fail(MUSPACE_ERANGE, "%s: dims exceed int32", fn);
   }
+  int64_t total = 0;
+  if (int rc = check_lengths(fn, valid_lens, num_cams, max_len, total)) return rc;
   if (batch == 0 || max_len == 0) return ok();
-  if (!grad_output || (valid_len > 0 && (!grad_slots || !index || !count))) {
+  if (!grad_output || (total > 0 && (!grad_slots || !index || !count))) {
     return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
   }
+  const CamDims c{batch, num_cams, max_len, num_query};
   hipStream_t st = static_cast<hipStream_t>(stream);
   with_dtypes(value_dtype, count_dtype, [&](auto vt, auto gt) {
-    launch_scatter_div_grad<decltype(vt), decltype(gt)>(grad_slots, index, count, grad_output, c,
-                                                        static_cast<int>(row), st);
+    launch_scatter_div_grad<decltype(vt), decltype(gt)>(grad_slots, index, valid_lens, count,
+                                                        grad_output, c, static_cast<int>(row),
+                                                        st);
   });
   return check_launch(fn);
 }

@@ -86,44 +86,100 @@ __device__ __forceinline__ Unit decode_unit(int u, const Shape &s) {
 template <typename VT>
 struct DenseRows {
   VT *out;
-  __device__ __forceinline__ int geo_row(int b, int q, int m, const Shape &s) const {
-    return (b * s.queries + q) * s.heads + m;
+  // geometry row of (b, q, m) and first value row of its slab
+  __device__ __forceinline__ void locate(int b, int q, int m, const Shape &s, int &row,
+                                         size_t &slab) const {
+    row = (b * s.queries + q) * s.heads + m;
+    slab = static_cast<size_t>(b) * s.spatial;
   }
-  __device__ __forceinline__ size_t slab(int b, const Shape &s) const {
-    return static_cast<size_t>(b) * s.spatial;
-  }
+  // what the epilogue of a unit loads ahead of time (nothing here)
+  static constexpr bool kLoadsAhead = false;
+  struct Ticket {};
+  __device__ __forceinline__ void fetch_index(Ticket &, int) const {}
+  __device__ __forceinline__ void fetch_count(Ticket &, int, const Shape &) const {}
   template <int C, int CPL>
   __device__ __forceinline__ void put(int b, int q, int m, int k, const float (&acc)[CPL],
-                                      const Shape &s) const {
-    store16(out + static_cast<size_t>(geo_row(b, q, m, s)) * C + k * CPL, acc);
+                                      const Ticket &, const Shape &s) const {
+    store16(out + static_cast<size_t>((b * s.queries + q) * s.heads + m) * C + k * CPL, acc);
   }
   __device__ __forceinline__ void put1(int b, int q, int m, int c, float acc,
                                        const Shape &s) const {
-    out[static_cast<size_t>(geo_row(b, q, m, s)) * s.channels + c] = from_float<VT>(acc);
+    out[static_cast<size_t>((b * s.queries + q) * s.heads + m) * s.channels + c] =
+        from_float<VT>(acc);
   }
 };
 
-// ScatterAverage: BEVFormer spatial cross-attention's epilogue for one camera,
-// fused into the forward (reference sketch: ms_deformable_im2col_scatter_div_*,
+constexpr int kMaxCams = 16;  // cameras per scatter-average launch
+
+// CameraSlots: BEVFormer spatial cross-attention's epilogue, fused into the
+// forward (reference sketch: ms_deformable_im2col_scatter_div_*,
 // /root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa_kernel.muh:419-486).
 // Value and geometry are camera-rebatched, [batch*cams, spatial, M, C] and
-// [batch*cams, max_len, M, L*P]; unit (b, q, m) is row q < valid_len of camera
-// `cam` in batch b, and its sums are added to the BEV query index[q]:
+// [batch*cams, max_len, M, L*P]. A launch covers cameras cam0 .. cam0+ncam-1;
+// their valid rows are numbered back to back, q = off[j] + r for row
+// r < off[j+1] - off[j] of camera cam0 + j, and index[q] is that row's BEV
+// query. Unit (b, q, m) adds its sums to slot (b, index[q], m):
 //   slots[b, index[q], m*C + c] += sum_c * (1 / count[b, index[q]]).
-// A camera's indices are distinct (one launch adds each slot at most once), so
-// the read-modify-write needs no atomics; cameras are launched in order. An
-// index outside [0, num_query) adds nothing.
-template <typename VT, typename CT>
-struct ScatterAverage {
+// kAtomic: the launch holds several cameras, which may share a slot, and adds
+// with fp32 global atomics (float slots only). Otherwise the launch holds one
+// camera, whose indices are distinct, and a plain read-modify-write suffices;
+// cameras are then launched in order. An index outside [0, num_query) adds
+// nothing. The row kernels cut the launch's blocks into one segment per
+// camera (blk[]), so that every block works on one camera (segment()).
+template <typename VT, typename GT, bool kAtomic>
+struct CameraSlots {
   VT *slots;             // [batch, num_query, M*C]
-  const int64_t *index;  // [valid_len] BEV query of each row of this camera
-  const CT *count;       // [batch, num_query], cameras that see the query
-  int cams, cam, max_len, num_query;
-  __device__ __forceinline__ int geo_row(int b, int q, int m, const Shape &s) const {
-    return ((b * cams + cam) * max_len + q) * s.heads + m;
+  const int64_t *index;  // [off[ncam]] BEV query of each valid row
+  const GT *count;       // [batch, num_query], cameras that see the query
+  int cams, cam0, ncam, max_len, num_query;
+  int off[kMaxCams + 1];  // first q of each camera of the launch; off[ncam] = valid rows
+  int blk[kMaxCams + 1];  // row kernels: first logical block of each camera's segment
+  static_assert(!kAtomic || std::is_same<VT, float>::value, "atomic slots are float32");
+
+  // The camera of logical block lb (uniform across the block: scalar code).
+  // Returns this policy narrowed to that camera, turns lb into the block's
+  // index inside the camera's segment and s into the camera's shape
+  // (s.queries = its valid rows).
+  __device__ __forceinline__ CameraSlots segment(int &lb, Shape &s) const {
+    int j = 0;
+#pragma unroll
+    for (int c = 1; c < kMaxCams; ++c) j = c < ncam && lb >= blk[c] ? c : j;
+    int first = 0, len = 0, b0 = 0;  // constant indices only
+#pragma unroll
+    for (int c = 0; c < kMaxCams; ++c) {
+      if (c == j) {
+        first = off[c];
+        len = off[c + 1] - off[c];
+        b0 = blk[c];
+      }
+    }
+    CameraSlots o = *this;
+    o.index = index + first;
+    o.cam0 = cam0 + j;
+    o.ncam = 1;
+    o.off[0] = 0;
+    o.off[1] = len;
+    s.queries = len;
+    s.units = s.batch * len * s.heads;
+    lb -= b0;
+    return o;
   }
-  __device__ __forceinline__ size_t slab(int b, const Shape &s) const {
-    return static_cast<size_t>(b * cams + cam) * s.spatial;
+
+  __device__ __forceinline__ void locate(int b, int q, int m, const Shape &s, int &row,
+                                         size_t &slab) const {
+    int j = 0, first = 0;  // constant indices only: off[] stays in scalar registers
+    if (ncam > 1) {
+#pragma unroll
+      for (int c = 1; c < kMaxCams; ++c) {
+        if (c < ncam && q >= off[c]) {
+          j = c;
+          first = off[c];
+        }
+      }
+    }
+    const int cam = cam0 + j;
+    row = ((b * cams + cam) * max_len + (q - first)) * s.heads + m;
+    slab = static_cast<size_t>(b * cams + cam) * s.spatial;
   }
   // slot row of (b, q, m) and the factor 1/count, or nullptr outside the grid
   __device__ __forceinline__ VT *slot(int b, int q, int m, const Shape &s, float &inv) const {
@@ -133,23 +189,47 @@ struct ScatterAverage {
     inv = 1.0f / to_float(count[bq]);
     return slots + (bq * s.heads + m) * s.channels;
   }
+  // A unit's BEV query and count, loaded ahead of its epilogue: the index one
+  // unit early, the count when the unit starts (before its gathers, so the
+  // in-order wait for the gathers covers it). Loads are unconditional with
+  // clamped offsets (q < s.queries always; count[0] exists: num_query > 0).
+  static constexpr bool kLoadsAhead = true;
+  struct Ticket {
+    int64_t bev;
+    float count;
+  };
+  __device__ __forceinline__ void fetch_index(Ticket &tk, int q) const { tk.bev = index[q]; }
+  __device__ __forceinline__ void fetch_count(Ticket &tk, int b, const Shape &s) const {
+    const bool ok = b < s.batch && tk.bev >= 0 && tk.bev < num_query;
+    tk.count = to_float(count[ok ? static_cast<int64_t>(b) * num_query + tk.bev : 0]);
+  }
   template <int C, int CPL>
   __device__ __forceinline__ void put(int b, int q, int m, int k, const float (&acc)[CPL],
-                                      const Shape &s) const {
-    float inv;
-    VT *row = slot(b, q, m, s, inv);
-    if (row == nullptr) return;
-    float cur[CPL];
-    load16(row + k * CPL, cur);
+                                      const Ticket &tk, const Shape &s) const {
+    if (tk.bev < 0 || tk.bev >= num_query) return;
+    const float inv = 1.0f / tk.count;
+    VT *row = slots + ((static_cast<int64_t>(b) * num_query + tk.bev) * s.heads + m) * C;
+    if constexpr (kAtomic) {
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) cur[c] += acc[c] * inv;
-    store16(row + k * CPL, cur);
+      for (int c = 0; c < CPL; ++c) unsafeAtomicAdd(row + k * CPL + c, acc[c] * inv);
+    } else {
+      float cur[CPL];
+      load16(row + k * CPL, cur);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) cur[c] += acc[c] * inv;
+      store16(row + k * CPL, cur);
+    }
   }
   __device__ __forceinline__ void put1(int b, int q, int m, int c, float acc,
                                        const Shape &s) const {
     float inv;
     VT *row = slot(b, q, m, s, inv);
-    if (row != nullptr) row[c] = from_float<VT>(to_float(row[c]) + acc * inv);
+    if (row == nullptr) return;
+    if constexpr (kAtomic) {
+      unsafeAtomicAdd(row + c, acc * inv);
+    } else {
+      row[c] = from_float<VT>(to_float(row[c]) + acc * inv);
+    }
   }
 };
 
@@ -169,7 +249,7 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
                                              const int64_t *__restrict__ starts,
                                              const GT *__restrict__ loc,
                                              const GT *__restrict__ attn, const Out &out,
-                                             const Shape &s, const RowPlan &plan) {
+                                             const Shape &s, const RowPlan &plan, int lb) {
   constexpr int CPL = RowTraits<VT>::kCpl;
   constexpr int VB = static_cast<int>(sizeof(VT));
   constexpr int KQ = C / CPL;
@@ -197,7 +277,6 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   u32x4 *my_off = tap_off + wave * kWave;
   float4 *my_w = tap_w + wave * kWave;
 
-  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const int64_t wave_id = static_cast<int64_t>(lb) * (kBlock / kWave) + wave;
   const int chunks = (s.lp + GU * NS - 1) / (GU * NS);
   const int steps = plan.iters * chunks;
@@ -205,9 +284,16 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   // geometry of this lane's tap sample in step st; the tap unit and the
   // output unit advance by UW units per wave iteration
   const int64_t u_first = wave_id * plan.iters * UW;
-  UnitIter tu, ou;
+  UnitIter tu, ou, on;  // on: the output unit after ou
   tu.init(u_first + tslot, s);
   ou.init(u_first + slot, s);
+  typename Out::Ticket tk_cur, tk_next;  // epilogue data of ou and on
+  if constexpr (Out::kLoadsAhead) {
+    on = ou;
+    on.advance(UW, s);
+    out.fetch_index(tk_cur, ou.q);
+    out.fetch_index(tk_next, on.q);
+  }
   float lx, ly, a;
   bool ok;
   int sm;
@@ -220,12 +306,14 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
     const int smp = s0 + tgi + GU * tj;
     ok = live && smp < s.lp;
     sm = ok ? smp : 0;
-    const size_t o = live ? static_cast<size_t>(out.geo_row(tu.b, tu.q, tu.m, s)) * s.lp + sm : 0;
+    int grow = 0;
+    size_t slab = 0;
+    if (live) out.locate(tu.b, tu.q, tu.m, s, grow, slab);
+    const size_t o = static_cast<size_t>(grow) * s.lp + sm;
     lx = to_float(loc[2 * o]);
     ly = to_float(loc[2 * o + 1]);
     a = to_float(attn[o]);
-    unit_base =
-        live ? static_cast<uint32_t>((out.slab(tu.b, s) * MC + tu.m * C) * VB) : 0u;
+    unit_base = static_cast<uint32_t>((slab * MC + tu.m * C) * VB);
   };
   load_geometry(0);
   float acc[CPL];
@@ -233,6 +321,7 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
 
   for (int st = 0; st < steps; ++st) {
+    if (st % chunks == 0) out.fetch_count(tk_cur, ou.b, s);
     // A. this lane's tap into the wavefront's table
     {
       const Level L = lv[level_of_sample(sm, s)];
@@ -283,8 +372,17 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
         for (int j = 0; j < CPL; ++j) acc[j] += __shfl_xor(acc[j], off, kWave);
       }
       const int64_t u64 = u_first + static_cast<int64_t>(st / chunks) * UW + slot;
-      if (u64 < s.units && gi == 0) out.template put<C, CPL>(ou.b, ou.q, ou.m, k, acc, s);
-      ou.advance(UW, s);
+      if (u64 < s.units && gi == 0) {
+        out.template put<C, CPL>(ou.b, ou.q, ou.m, k, acc, tk_cur, s);
+      }
+      if constexpr (Out::kLoadsAhead) {
+        ou = on;
+        tk_cur = tk_next;
+        on.advance(UW, s);
+        out.fetch_index(tk_next, on.q);
+      } else {
+        ou.advance(UW, s);
+      }
 #pragma unroll
       for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
     }
@@ -298,19 +396,23 @@ __global__ void __launch_bounds__(kBlock)
                       const GT *__restrict__ loc, const GT *__restrict__ attn,
                       VT *__restrict__ out, Shape s, RowPlan plan) {
   forward_rows<VT, GT, C, NS>(value, value_bytes, shapes, starts, loc, attn, DenseRows<VT>{out},
-                              s, plan);
+                              s, plan, xcd_logical_block(blockIdx.x, gridDim.x));
 }
 
-// One camera of the spatial cross-attention, summed into the BEV slots
-// (ScatterAverage above); s.batch, s.queries are the batch and valid_len.
-template <typename VT, typename GT, int C, int NS>
+// Cameras of the spatial cross-attention, summed into the BEV slots
+// (CameraSlots above); s.batch is the batch. Each camera's units take the
+// logical blocks [out.blk[j], out.blk[j+1]).
+template <typename VT, typename GT, int C, int NS, bool kAtomic>
 __global__ void __launch_bounds__(kBlock)
     msda_forward_scatter_div_rows(const VT *__restrict__ value, uint32_t value_bytes,
                                   const int64_t *__restrict__ shapes,
                                   const int64_t *__restrict__ starts, const GT *__restrict__ loc,
-                                  const GT *__restrict__ attn, ScatterAverage<VT, GT> out,
+                                  const GT *__restrict__ attn, CameraSlots<VT, GT, kAtomic> out,
                                   Shape s, RowPlan plan) {
-  forward_rows<VT, GT, C, NS>(value, value_bytes, shapes, starts, loc, attn, out, s, plan);
+  int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  Shape sc = s;
+  const CameraSlots<VT, GT, kAtomic> cam = out.segment(lb, sc);
+  forward_rows<VT, GT, C, NS>(value, value_bytes, shapes, starts, loc, attn, cam, sc, plan, lb);
 }
 
 // ------------------------------------------------------------ backward ---
@@ -454,8 +556,10 @@ __device__ __forceinline__ void forward_generic(const VT *__restrict__ value,
     const int m = si % s.heads;
     const int q = (si / s.heads) % s.queries;
     const int b = si / (s.heads * s.queries);
-    const int row = out.geo_row(b, q, m, s);
-    const VT *vbase = value + out.slab(b, s) * MC + m * C + c;
+    int row;
+    size_t slab;
+    out.locate(b, q, m, s, row, slab);
+    const VT *vbase = value + slab * MC + m * C + c;
     const GT *lbase = loc + static_cast<size_t>(row) * s.lp * 2;
     const GT *abase = attn + static_cast<size_t>(row) * s.lp;
     float acc = 0.0f;
@@ -483,45 +587,63 @@ __global__ void __launch_bounds__(kBlock)
   forward_generic<VT, GT>(value, shapes, starts, loc, attn, DenseRows<VT>{out}, s);
 }
 
-template <typename VT, typename GT>
+template <typename VT, typename GT, bool kAtomic>
 __global__ void __launch_bounds__(kBlock)
     msda_forward_scatter_div_generic(const VT *__restrict__ value,
                                      const int64_t *__restrict__ shapes,
                                      const int64_t *__restrict__ starts,
                                      const GT *__restrict__ loc, const GT *__restrict__ attn,
-                                     ScatterAverage<VT, GT> out, Shape s) {
+                                     CameraSlots<VT, GT, kAtomic> out, Shape s) {
   forward_generic<VT, GT>(value, shapes, starts, loc, attn, out, s);
 }
 
-// Backward of one camera's scatter-average: the gradient of the camera's MSDA
-// output rows, grad_out[(b*cams + cam)*max_len + r][row] =
-// grad_slots[b, index[r]][row] / count[b, index[r]] for r < valid_len; rows
-// past valid_len (the rebatch padding) and indices outside [0, num_query) get
-// zeros. W = 16 / sizeof(VT) elements per thread (16-byte rows) or 1.
+// Valid rows of each camera: camera c's rows r < len[c] are q = off[c] + r of
+// the concatenated index.
+struct CameraRows {
+  int off[kMaxCams], len[kMaxCams];
+};
+
+// Backward of the scatter-average: the gradient of the cameras' MSDA output
+// rows, grad_out[(b*cams + cam)*max_len + r][row] =
+// grad_slots[b, index[off[cam] + r]][row] / count[b, index[off[cam] + r]] for
+// r < len[cam]; rows past len[cam] (the rebatch padding) and indices outside
+// [0, num_query) get zeros. Grid row blockIdx.y handles camera cam0 +
+// blockIdx.y, so the table lookup is uniform across a block; W = 16 /
+// sizeof(VT) elements per thread (16-byte rows) or 1.
 template <typename VT, typename GT, int W>
 __global__ void __launch_bounds__(kBlock)
     msda_scatter_div_grad(const VT *__restrict__ grad_slots, const int64_t *__restrict__ index,
                           const GT *__restrict__ count, VT *__restrict__ grad_out, int batch,
-                          int cams, int cam, int valid_len, int max_len, int num_query,
+                          int cams, int cam0, CameraRows rows, int max_len, int num_query,
                           int row) {
   static_assert(W == 1 || W * sizeof(VT) == 16, "one element or one 16-byte chunk per thread");
+  const int j = blockIdx.y;
+  int off = 0, valid = 0;
+#pragma unroll
+  for (int c = 0; c < kMaxCams; ++c) {
+    if (c == j) {
+      off = rows.off[c];
+      valid = rows.len[c];
+    }
+  }
+  const int cam = cam0 + j;
   const int per_row = row / W;
   const int64_t total = static_cast<int64_t>(batch) * max_len * per_row;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int j = static_cast<int>(i % per_row);
+    const int e0 = static_cast<int>(i % per_row);
     const int64_t br = i / per_row;
     const int r = static_cast<int>(br % max_len);
     const int b = static_cast<int>(br / max_len);
     float v[W];
 #pragma unroll
     for (int e = 0; e < W; ++e) v[e] = 0.0f;
-    if (r < valid_len) {
-      const int64_t bev = index[r];
+    if (r < valid) {
+      const int64_t bev = index[off + r];
       if (bev >= 0 && bev < num_query) {
         const int64_t bq = static_cast<int64_t>(b) * num_query + bev;
         const float inv = 1.0f / to_float(count[bq]);
-        const VT *src = grad_slots + bq * row + static_cast<int64_t>(j) * W;
+        const VT *src = grad_slots + bq * row + static_cast<int64_t>(e0) * W;
         if constexpr (W == 1) {
           v[0] = to_float(src[0]);
         } else {
@@ -532,7 +654,7 @@ __global__ void __launch_bounds__(kBlock)
       }
     }
     VT *dst = grad_out + (static_cast<int64_t>(b * cams + cam) * max_len + r) * row +
-              static_cast<int64_t>(j) * W;
+              static_cast<int64_t>(e0) * W;
     if constexpr (W == 1) {
       dst[0] = from_float<VT>(v[0]);
     } else {

@@ -13,7 +13,10 @@ with its host wrapper ``ms_deformable_im2col_scatter_div_musa``
 launch per camera adds ``MSDA(row) * (1 / count[bev])`` straight into
 ``slots[bev]``, so the per-camera output never reaches memory. This operator
 keeps that arithmetic (each camera's sum is scaled by ``1/count`` and then
-added, cameras in order) and adds the backward the reference lacks: the
+added) but runs all cameras in one launch (``ms_deform_attn_forward_scatter_div_cams``):
+float32 slots take the cameras' adds as fp32 atomics, so one launch fills the
+GPU where six per-camera launches each leave a tail; 16-bit slots keep one
+ordered launch per camera. It also adds the backward the reference lacks: the
 gradient of a camera's output row is ``grad_slots[b, bev] / count[b, bev]``
 (``ms_deform_attn_scatter_div_grad``), after which the MSDA backward gives
 the value, location and weight gradients.
@@ -43,7 +46,6 @@ class _ScatterDivFunction(torch.autograd.Function):
         ext = _native_extension()
         if ext is None:
             raise RuntimeError("muSPACE HIP native library is unavailable")
-        num_cams = len(indexes)
         geometry = _native_geometry_dtype(value, sampling_locations, attention_weights)
         value_arg = value.contiguous()
         sampling_arg = sampling_locations.to(geometry).contiguous()
@@ -51,17 +53,17 @@ class _ScatterDivFunction(torch.autograd.Function):
         count_arg = count.to(geometry).contiguous()
         spatial_arg = spatial_shapes.contiguous()
         start_arg = level_start_index.contiguous()
-        index_args = tuple(index.contiguous() for index in indexes)
-        for cam, index in enumerate(index_args):  # in camera order, as the reference launches
-            ext.ms_deform_attn_forward_scatter_div(
-                value_arg, spatial_arg, start_arg, sampling_arg, attn_arg, index, count_arg,
-                slots, num_cams, cam,
-            )
+        lens = [int(index.numel()) for index in indexes]
+        index_arg = torch.cat([index.reshape(-1) for index in indexes])
+        ext.ms_deform_attn_forward_scatter_div_cams(
+            value_arg, spatial_arg, start_arg, sampling_arg, attn_arg, index_arg, lens, count_arg,
+            slots,
+        )
         ctx.mark_dirty(slots)
-        ctx.num_cams = num_cams
+        ctx.lens = lens
         ctx.dtypes = (value.dtype, sampling_locations.dtype, attention_weights.dtype)
         ctx.save_for_backward(value_arg, spatial_arg, start_arg, sampling_arg, attn_arg, count_arg,
-                              *index_args)
+                              index_arg)
         return slots
 
     @staticmethod
@@ -69,7 +71,7 @@ class _ScatterDivFunction(torch.autograd.Function):
         ext = _native_extension()
         if ext is None:
             raise RuntimeError("muSPACE HIP native library is unavailable")
-        value, spatial_shapes, level_start_index, sampling, attention, count, *indexes = (
+        value, spatial_shapes, level_start_index, sampling, attention, count, index = (
             ctx.saved_tensors
         )
         rows, max_len = sampling.shape[0], sampling.shape[1]
@@ -77,8 +79,7 @@ class _ScatterDivFunction(torch.autograd.Function):
         grad = grad_slots.to(value.dtype).contiguous()
         # every row of every camera is written (zeros past each camera's valid rows)
         grad_rows = torch.empty((rows, max_len, row), dtype=value.dtype, device=value.device)
-        for cam, index in enumerate(indexes):
-            ext.ms_deform_attn_scatter_div_grad(grad, index, count, grad_rows, ctx.num_cams, cam)
+        ext.ms_deform_attn_scatter_div_grad(grad, index, ctx.lens, count, grad_rows)
         grad_value = torch.empty(value.shape, dtype=torch.float32, device=value.device)
         grad_sampling = torch.empty(sampling.shape, dtype=torch.float32, device=value.device)
         grad_attention = torch.empty(attention.shape, dtype=torch.float32, device=value.device)
@@ -94,7 +95,7 @@ class _ScatterDivFunction(torch.autograd.Function):
             grad_attention.to(attention_dtype),
             None,
             grad_slots,
-            *([None] * len(indexes)),
+            *([None] * len(ctx.lens)),
         )
 
 

@@ -63,9 +63,15 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         + [_c_int64] * 11
         + [_c_ptr],
     ),
+    "ms_deform_attn_forward_scatter_div_cams": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 9
+        + [_c_ptr],
+    ),
     "ms_deform_attn_scatter_div_grad": (
         _c_int,
-        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_ptr] + [_c_int64] * 7 + [_c_ptr],
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr] + [_c_int64] * 5 + [_c_ptr],
     ),
 }
 
@@ -129,6 +135,7 @@ class NativeLibrary:
             "ms_deform_attn_forward": self.ms_deform_attn_forward,
             "ms_deform_attn_backward": self.ms_deform_attn_backward,
             "ms_deform_attn_forward_scatter_div": self.ms_deform_attn_forward_scatter_div,
+            "ms_deform_attn_forward_scatter_div_cams": self.ms_deform_attn_forward_scatter_div_cams,
             "ms_deform_attn_scatter_div_grad": self.ms_deform_attn_scatter_div_grad,
             "add_one": self.add_one,
         }
@@ -312,12 +319,69 @@ class NativeLibrary:
             )
         self._raise_on(rc, "ms_deform_attn_forward_scatter_div")
 
-    def ms_deform_attn_scatter_div_grad(
-        self, grad_slots, index, count, grad_output, num_cams: int, cam_id: int,
+    def ms_deform_attn_forward_scatter_div_cams(
+        self, value, spatial_shapes, level_start_index, sampling_locations,
+        attention_weights, index, valid_lens, count, slots,
     ) -> None:
-        """Camera cam_id's rows of grad_output ``[bs*num_cams, max_len, row]`` from
-        grad_slots ``[bs, num_query, row]``: ``grad_slots[b, index[r]] / count[b,
-        index[r]]`` for r < len(index), zero past it."""
+        """Every camera of the spatial cross-attention added into ``slots`` in place.
+
+        As :meth:`ms_deform_attn_forward_scatter_div` for cameras 0..num_cams-1,
+        with ``index`` the cameras' BEV ids concatenated and ``valid_lens`` (a
+        sequence of ints, one per camera) their lengths.
+        """
+        import torch
+
+        half = (torch.float32, torch.float16, torch.bfloat16)
+        _check(value, "value", half)
+        _check(spatial_shapes, "spatial_shapes", (torch.int64,))
+        _check(level_start_index, "level_start_index", (torch.int64,))
+        geom = (torch.float32,) if value.dtype == torch.float32 else (torch.float32, value.dtype)
+        _check(sampling_locations, "sampling_locations", geom)
+        _check(attention_weights, "attention_weights", (sampling_locations.dtype,))
+        _check(index, "index", (torch.int64,))
+        _check(count, "count", (sampling_locations.dtype,))
+        _check(slots, "slots", (value.dtype,))
+        if value.dim() != 4 or sampling_locations.dim() != 6 or index.dim() != 1:
+            raise RuntimeError("value must be 4-D, sampling_locations 6-D and index 1-D")
+        if slots.dim() != 3:
+            raise RuntimeError("slots must be 3-D [batch, num_query, num_heads*channels]")
+        lens = [int(n) for n in valid_lens]
+        num_cams = len(lens)
+        rows, spatial, heads, channels = value.shape
+        if num_cams <= 0 or rows % num_cams != 0:
+            raise RuntimeError(f"value rows {rows} are not a multiple of num_cams {num_cams}")
+        if sum(lens) != index.shape[0]:
+            raise RuntimeError(
+                f"index has {index.shape[0]} entries, valid_lens sum to {sum(lens)}")
+        batch, num_query = rows // num_cams, slots.shape[1]
+        levels = spatial_shapes.shape[0]
+        max_len, points = sampling_locations.shape[1], sampling_locations.shape[4]
+        _check_shape(spatial_shapes, "spatial_shapes", (levels, 2))
+        _check_shape(level_start_index, "level_start_index", (levels,))
+        _check_shape(sampling_locations, "sampling_locations",
+                     (rows, max_len, heads, levels, points, 2))
+        _check_shape(attention_weights, "attention_weights", (rows, max_len, heads, levels, points))
+        _check_shape(count, "count", (batch, num_query))
+        _check_shape(slots, "slots", (batch, num_query, heads * channels))
+        host_lens = (ctypes.c_int64 * num_cams)(*lens)
+        with torch.cuda.device(value.device):
+            rc = self._raw["ms_deform_attn_forward_scatter_div_cams"](
+                value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
+                level_start_index.data_ptr(), sampling_locations.data_ptr(),
+                attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
+                index.data_ptr(), ctypes.cast(host_lens, ctypes.c_void_p), count.data_ptr(),
+                slots.data_ptr(), batch, num_cams, spatial, heads, channels, levels, max_len,
+                points, num_query, self._stream(value),
+            )
+        self._raise_on(rc, "ms_deform_attn_forward_scatter_div_cams")
+
+    def ms_deform_attn_scatter_div_grad(
+        self, grad_slots, index, valid_lens, count, grad_output,
+    ) -> None:
+        """grad_output ``[bs*num_cams, max_len, row]`` from grad_slots ``[bs,
+        num_query, row]``: camera c's row r gets ``grad_slots[b, q] / count[b, q]``
+        (q its BEV id in the concatenated ``index``) for r < valid_lens[c], zero
+        past it."""
         import torch
 
         half = (torch.float32, torch.float16, torch.bfloat16)
@@ -329,16 +393,22 @@ class NativeLibrary:
         _check(grad_output, "grad_output", (grad_slots.dtype,))
         if grad_slots.dim() != 3 or grad_output.dim() != 3 or index.dim() != 1:
             raise RuntimeError("grad_slots and grad_output must be 3-D and index 1-D")
+        lens = [int(n) for n in valid_lens]
+        num_cams = len(lens)
+        if num_cams <= 0 or sum(lens) != index.shape[0]:
+            raise RuntimeError(
+                f"index has {index.shape[0]} entries, valid_lens sum to {sum(lens)}")
         batch, num_query, row = grad_slots.shape
-        rows, max_len = grad_output.shape[0], grad_output.shape[1]
+        max_len = grad_output.shape[1]
         _check_shape(grad_output, "grad_output", (batch * num_cams, max_len, row))
         _check_shape(count, "count", (batch, num_query))
+        host_lens = (ctypes.c_int64 * num_cams)(*lens)
         with torch.cuda.device(grad_slots.device):
             rc = self._raw["ms_deform_attn_scatter_div_grad"](
                 grad_slots.data_ptr(), _dtype_code(grad_slots.dtype), index.data_ptr(),
-                count.data_ptr(), _dtype_code(count.dtype), grad_output.data_ptr(), batch,
-                num_cams, int(cam_id), index.shape[0], max_len, num_query, row,
-                self._stream(grad_slots),
+                ctypes.cast(host_lens, ctypes.c_void_p), count.data_ptr(),
+                _dtype_code(count.dtype), grad_output.data_ptr(), batch, num_cams, max_len,
+                num_query, row, self._stream(grad_slots),
             )
         self._raise_on(rc, "ms_deform_attn_scatter_div_grad")
 

@@ -147,3 +147,51 @@ def test_rejects_cpu_tensors_and_bad_indexes():
     with pytest.raises(RuntimeError, match="num_cams"):
         multi_scale_deformable_attn_scatter_div(value, shapes, starts, loc, attn,
                                                 indexes + indexes[:1], count)
+
+
+@pytest.mark.parametrize("value_dtype", [torch.float32, torch.bfloat16])
+def test_per_camera_entry_point_matches_the_all_camera_call(value_dtype):
+    """The reference's interface (one ordered launch per camera) against the
+    all-camera call the operator uses."""
+    from muspace_amd.runtime.native import load_native_module
+
+    lib = load_native_module()
+    case = scatter_div_case(14, batch=2, cams=5, max_len=11, num_query=30, heads=4,
+                            channels=32, levels=((7, 6), (4, 3)), points=4, out_of_range=True)
+    value, shapes, starts, loc, attn, indexes, count, slots = _device_case(
+        case, value_dtype, value_dtype)
+    per_camera = slots.clone()
+    for cam, index in enumerate(indexes):
+        lib.ms_deform_attn_forward_scatter_div(value, shapes, starts, loc, attn, index, count,
+                                               per_camera, len(indexes), cam)
+    together = slots.clone()
+    lib.ms_deform_attn_forward_scatter_div_cams(value, shapes, starts, loc, attn,
+                                                torch.cat(indexes), [len(i) for i in indexes],
+                                                count, together)
+    tol = 1e-5 if value_dtype == torch.float32 else 0.0
+    torch.testing.assert_close(together, per_camera, rtol=tol, atol=tol)
+    expected = msda_scatter_div.scatter_div(*_oracle_inputs(
+        (value, shapes, starts, loc, attn, indexes, count, slots)))
+    tol = 1e-5 if value_dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(together.float().cpu(), expected, rtol=tol, atol=tol)
+
+
+def test_more_cameras_than_one_launch_holds():
+    """17 cameras: the all-camera call splits them over two launches."""
+    case = scatter_div_case(15, batch=1, cams=17, max_len=6, num_query=50, heads=2,
+                            channels=16, levels=((5, 4),), points=2, dtype=torch.float32)
+    dev = _device_case(case, torch.float32, torch.float32)
+    value, shapes, starts, loc, attn, indexes, count, slots = dev
+    for t in (value, loc, attn):
+        t.requires_grad_(True)
+    ref = [t.clone().requires_grad_(t.is_floating_point()) if i != 4 else t
+           for i, t in enumerate(_oracle_inputs(dev))]
+    out = multi_scale_deformable_attn_scatter_div(value, shapes, starts, loc, attn, indexes,
+                                                  count, slots.clone())
+    expected = msda_scatter_div.scatter_div(*ref)
+    torch.testing.assert_close(out.detach().cpu(), expected.detach(), rtol=1e-5, atol=1e-5)
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(4))
+    (out * g.to(DEV)).sum().backward()
+    (expected * g).sum().backward()
+    for native, cpu in ((value, ref[0]), (loc, ref[2]), (attn, ref[3])):
+        torch.testing.assert_close(native.grad.cpu(), cpu.grad, rtol=1e-4, atol=1e-4)
