@@ -17,11 +17,15 @@ from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_DIR = PACKAGE_DIR.parent
-SOURCES = (PACKAGE_DIR / "csrc" / "msda_capi.hip",)
+SOURCES = (PACKAGE_DIR / "csrc" / "msda_capi.hip", PACKAGE_DIR / "csrc" / "dfa_capi.hip")
 DEPENDS = (
+    PACKAGE_DIR / "csrc" / "capi_errors.hpp",
     PACKAGE_DIR / "csrc" / "msda_device.hpp",
     PACKAGE_DIR / "csrc" / "msda_kernels.hpp",
+    PACKAGE_DIR / "csrc" / "msda_backward_tiles.hpp",
+    PACKAGE_DIR / "csrc" / "dfa_kernels.hpp",
     REPO_DIR / "include" / "muspace_msda.h",
+    REPO_DIR / "include" / "muspace_dfa.h",
 )
 LIBRARY = PACKAGE_DIR / "native" / "libmuspace_msda.so"
 OFFLOAD_ARCH = "gfx950"

@@ -17,33 +17,15 @@
 #include <cstdio>
 
 #include "../../include/muspace_msda.h"
+#include "capi_errors.hpp"
 #include "msda_backward_tiles.hpp"
 #include "msda_kernels.hpp"
 
 namespace {
 
-thread_local char g_error[512] = "";
-
-int fail(int code, const char *fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_error, sizeof(g_error), fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-int ok() {
-  g_error[0] = '\0';
-  return MUSPACE_OK;
-}
-
-int check_launch(const char *what) {
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    return fail(MUSPACE_ELAUNCH, "%s: kernel launch failed: %s", what, hipGetErrorString(e));
-  }
-  return ok();
-}
+using capi::check_launch;
+using capi::fail;
+using capi::ok;
 
 struct Args {
   int64_t batch, spatial, heads, channels, levels, queries, points, step;
@@ -1016,7 +998,7 @@ int add_one(const float *x, float *y, int64_t n, void *stream) {
   return check_launch("add_one");
 }
 
-const char *muspace_last_error(void) { return g_error; }
+const char *muspace_last_error(void) { return capi::g_error; }
 
 int muspace_abi_version(void) { return MUSPACE_MSDA_ABI_VERSION; }
 

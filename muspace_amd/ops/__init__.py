@@ -8,8 +8,18 @@ from .multi_scale_deformable_attn import (
     multi_scale_deformable_attn_pytorch_compat,
 )
 from .scatter_div import multi_scale_deformable_attn_scatter_div
+from .deformable_aggregation import (
+    deformable_aggregation,
+    deformable_aggregation_function,
+    deformable_aggregation_reference,
+    feature_maps_format,
+)
 
 __all__ = [
+    "deformable_aggregation",
+    "deformable_aggregation_function",
+    "deformable_aggregation_reference",
+    "feature_maps_format",
     "explain_dispatch",
     "level_start_index_from_shapes",
     "multi_scale_deformable_attn",

@@ -73,6 +73,11 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         _c_int,
         [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr] + [_c_int64] * 5 + [_c_ptr],
     ),
+    # include/muspace_dfa.h
+    "deformable_aggregation_forward_opt": (_c_int, [_c_ptr] * 6 + [_c_int64] * 8 + [_c_ptr]),
+    "deformable_aggregation_forward_base": (_c_int, [_c_ptr] * 6 + [_c_int64] * 8 + [_c_ptr]),
+    "deformable_aggregation_backward_opt": (_c_int, [_c_ptr] * 9 + [_c_int64] * 8 + [_c_ptr]),
+    "deformable_aggregation_backward_base": (_c_int, [_c_ptr] * 9 + [_c_int64] * 8 + [_c_ptr]),
 }
 
 
@@ -136,6 +141,10 @@ class NativeLibrary:
             "ms_deform_attn_backward": self.ms_deform_attn_backward,
             "ms_deform_attn_forward_scatter_div": self.ms_deform_attn_forward_scatter_div,
             "ms_deform_attn_forward_scatter_div_cams": self.ms_deform_attn_forward_scatter_div_cams,
+            "deformable_aggregation_forward_opt": self.deformable_aggregation_forward_opt,
+            "deformable_aggregation_forward_base": self.deformable_aggregation_forward_base,
+            "deformable_aggregation_backward_opt": self.deformable_aggregation_backward_opt,
+            "deformable_aggregation_backward_base": self.deformable_aggregation_backward_base,
             "ms_deform_attn_scatter_div_grad": self.ms_deform_attn_scatter_div_grad,
             "add_one": self.add_one,
         }
@@ -411,6 +420,104 @@ class NativeLibrary:
                 num_query, row, self._stream(grad_slots),
             )
         self._raise_on(rc, "ms_deform_attn_scatter_div_grad")
+
+    # ------------------------------------------------ deformable aggregation ---
+    @staticmethod
+    def _dfa_dims(mc_ms_feat, spatial_shape, scale_start_index, sampling_location, weights):
+        """Checks of the reference's validate() (deformable_aggregation_musa.mu:669-679)
+        and the dims its launchers read (:660-668)."""
+        import torch
+
+        _check(mc_ms_feat, "mc_ms_feat", (torch.float32,))
+        _check(spatial_shape, "spatial_shape", (torch.int32,))
+        _check(scale_start_index, "scale_start_index", (torch.int32,))
+        _check(sampling_location, "sampling_location", (torch.float32,))
+        _check(weights, "weights", (torch.float32,))
+        if (mc_ms_feat.dim() != 3 or spatial_shape.dim() != 3 or sampling_location.dim() != 5
+                or weights.dim() != 6):
+            raise RuntimeError("mc_ms_feat must be 3-D, spatial_shape 3-D, sampling_location "
+                               "5-D and weights 6-D")
+        batch, num_feat, num_embeds = mc_ms_feat.shape
+        num_cams, num_scale = spatial_shape.shape[0], spatial_shape.shape[1]
+        num_anchors, num_pts = sampling_location.shape[1], sampling_location.shape[2]
+        num_groups = weights.shape[5]
+        _check_shape(spatial_shape, "spatial_shape", (num_cams, num_scale, 2))
+        _check_shape(scale_start_index, "scale_start_index", (num_cams, num_scale))
+        _check_shape(sampling_location, "sampling_location",
+                     (batch, num_anchors, num_pts, num_cams, 2))
+        _check_shape(weights, "weights",
+                     (batch, num_anchors, num_pts, num_cams, num_scale, num_groups))
+        return (batch, num_cams, num_feat, num_embeds, num_scale, num_anchors, num_pts,
+                num_groups)
+
+    def _dfa_forward(self, name, mc_ms_feat, spatial_shape, scale_start_index,
+                     sampling_location, weights, output) -> None:
+        import torch
+
+        dims = self._dfa_dims(mc_ms_feat, spatial_shape, scale_start_index, sampling_location,
+                              weights)
+        _check(output, "out", (torch.float32,))
+        _check_shape(output, "out", (dims[0], dims[5], dims[3]))
+        with torch.cuda.device(mc_ms_feat.device):
+            rc = self._raw[name](
+                mc_ms_feat.data_ptr(), spatial_shape.data_ptr(), scale_start_index.data_ptr(),
+                sampling_location.data_ptr(), weights.data_ptr(), output.data_ptr(), *dims,
+                self._stream(mc_ms_feat),
+            )
+        self._raise_on(rc, name)
+
+    def _dfa_backward(self, name, mc_ms_feat, spatial_shape, scale_start_index,
+                      sampling_location, weights, grad_output, grad_mc_ms_feat,
+                      grad_sampling_location, grad_weights) -> None:
+        import torch
+
+        dims = self._dfa_dims(mc_ms_feat, spatial_shape, scale_start_index, sampling_location,
+                              weights)
+        for tensor, label, like in (
+            (grad_output, "grad_output", (dims[0], dims[5], dims[3])),
+            (grad_mc_ms_feat, "grad_mc_ms_feat", tuple(mc_ms_feat.shape)),
+            (grad_sampling_location, "grad_sampling_location", tuple(sampling_location.shape)),
+            (grad_weights, "grad_weights", tuple(weights.shape)),
+        ):
+            _check(tensor, label, (torch.float32,))
+            _check_shape(tensor, label, like)
+        with torch.cuda.device(mc_ms_feat.device):
+            rc = self._raw[name](
+                mc_ms_feat.data_ptr(), spatial_shape.data_ptr(), scale_start_index.data_ptr(),
+                sampling_location.data_ptr(), weights.data_ptr(), grad_output.data_ptr(),
+                grad_mc_ms_feat.data_ptr(), grad_sampling_location.data_ptr(),
+                grad_weights.data_ptr(), *dims, self._stream(mc_ms_feat),
+            )
+        self._raise_on(rc, name)
+
+    def deformable_aggregation_forward_opt(self, mc_ms_feat, spatial_shape, scale_start_index,
+                                           sampling_location, weights, output) -> None:
+        """output += aggregation (reference argument order, deformable_aggregation_musa.mu:717)."""
+        self._dfa_forward("deformable_aggregation_forward_opt", mc_ms_feat, spatial_shape,
+                          scale_start_index, sampling_location, weights, output)
+
+    def deformable_aggregation_forward_base(self, mc_ms_feat, spatial_shape, scale_start_index,
+                                            sampling_location, weights, output) -> None:
+        self._dfa_forward("deformable_aggregation_forward_base", mc_ms_feat, spatial_shape,
+                          scale_start_index, sampling_location, weights, output)
+
+    def deformable_aggregation_backward_opt(self, mc_ms_feat, spatial_shape, scale_start_index,
+                                            sampling_location, weights, grad_output,
+                                            grad_mc_ms_feat, grad_sampling_location,
+                                            grad_weights) -> None:
+        """grad_mc_ms_feat += ...; location and weight gradients written
+        (reference argument order, deformable_aggregation_musa.mu:725)."""
+        self._dfa_backward("deformable_aggregation_backward_opt", mc_ms_feat, spatial_shape,
+                           scale_start_index, sampling_location, weights, grad_output,
+                           grad_mc_ms_feat, grad_sampling_location, grad_weights)
+
+    def deformable_aggregation_backward_base(self, mc_ms_feat, spatial_shape,
+                                             scale_start_index, sampling_location, weights,
+                                             grad_output, grad_mc_ms_feat,
+                                             grad_sampling_location, grad_weights) -> None:
+        self._dfa_backward("deformable_aggregation_backward_base", mc_ms_feat, spatial_shape,
+                           scale_start_index, sampling_location, weights, grad_output,
+                           grad_mc_ms_feat, grad_sampling_location, grad_weights)
 
     def add_one(self, value, actual) -> None:
         """Build smoke: actual = value + 1 (float32 device tensors)."""

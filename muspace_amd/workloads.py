@@ -231,3 +231,69 @@ def sca_algorithmic_bytes(valid_rows: int, cameras: int, num_query: int,
     row = cfg.heads * cfg.channels
     slots = (cfg.batch // cameras) * num_query * row
     return 4 * n_value + valid_rows * (4 * 3 * per_row + 8 + 4) + 2 * 4 * slots
+
+
+# --------------------------------------------------- deformable aggregation ---
+
+# SparseDrive's production shape, as the reference's benchmark case defines it
+# (/root/reference/benchmarks/deformable_aggregation/deformable_aggregation_case.py:30-54):
+# 8 samples, 6 cameras x 4 scales of (64,176)..(8,22) maps, 256 channels in 8
+# groups, 900 anchors x 13 points, 18.6% of (anchor, point, camera) inside (0, 1).
+DFA_BATCH, DFA_CAMS, DFA_ANCHORS, DFA_PTS, DFA_GROUPS, DFA_CHANNELS = 8, 6, 900, 13, 8, 256
+DFA_SCALES = ((64, 176), (32, 88), (16, 44), (8, 22))
+DFA_ACTIVE_FRAC = 0.18635328114032745
+DFA_WEIGHT_SCALE = 0.004
+
+
+def make_dfa_inputs(
+    *,
+    seed: int = DEFAULT_SEED,
+    device: str | torch.device = "cpu",
+    active_frac: float = DFA_ACTIVE_FRAC,
+) -> dict[str, torch.Tensor]:
+    """Seeded SparseDrive-shaped inputs. Drawn on the CPU in the order feature
+    maps ~ N(0,1), active mask, outside points ~ 10*N(0,1), inside points
+    ~ U(0.01, 0.99), weights ~ 0.004*U(0,1), then grad_output ~ N(0,1)."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    per_cam = sum(h * w for h, w in DFA_SCALES)
+    num_feat = DFA_CAMS * per_cam
+    starts, offset = [], 0
+    for _ in range(DFA_CAMS):
+        row = []
+        for h, w in DFA_SCALES:
+            row.append(offset)
+            offset += h * w
+        starts.append(row)
+    point_shape = (DFA_BATCH, DFA_ANCHORS, DFA_PTS, DFA_CAMS)
+    feat = torch.randn((DFA_BATCH, num_feat, DFA_CHANNELS), generator=gen)
+    active = torch.rand(point_shape, generator=gen) < active_frac
+    outside = torch.randn(*point_shape, 2, generator=gen) * 10.0
+    inside = torch.rand(*point_shape, 2, generator=gen) * 0.98 + 0.01
+    loc = torch.where(active.unsqueeze(-1), inside, outside)
+    weights = torch.rand((*point_shape, len(DFA_SCALES), DFA_GROUPS), generator=gen)
+    weights = weights * DFA_WEIGHT_SCALE
+    grad = torch.randn((DFA_BATCH, DFA_ANCHORS, DFA_CHANNELS), generator=gen)
+    return {
+        "mc_ms_feat": feat.to(device),
+        "spatial_shape": torch.tensor([list(map(list, DFA_SCALES))] * DFA_CAMS,
+                                      dtype=torch.int32).to(device),
+        "scale_start_index": torch.tensor(starts, dtype=torch.int32).to(device),
+        "sampling_location": loc.to(device),
+        "weights": weights.to(device),
+        "grad_output": grad.to(device),
+    }
+
+
+def dfa_algorithmic_bytes() -> tuple[int, int]:
+    """(forward, backward) bytes of the SparseDrive shape, every tensor once:
+    fwd = |feat| + |loc| + |weights| + |out|; bwd adds |grad_out| and the three
+    gradients (float32) to the inputs."""
+    per_cam = sum(h * w for h, w in DFA_SCALES)
+    n_feat = DFA_BATCH * DFA_CAMS * per_cam * DFA_CHANNELS
+    n_pts = DFA_BATCH * DFA_ANCHORS * DFA_PTS * DFA_CAMS
+    n_loc = 2 * n_pts
+    n_w = n_pts * len(DFA_SCALES) * DFA_GROUPS
+    n_out = DFA_BATCH * DFA_ANCHORS * DFA_CHANNELS
+    fwd = 4 * (n_feat + n_loc + n_w + n_out)
+    bwd = 4 * (n_feat + n_loc + n_w + n_out + n_feat + n_loc + n_w)
+    return fwd, bwd

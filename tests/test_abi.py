@@ -14,17 +14,23 @@ from muspace_amd.runtime import native
 
 ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "muspace_msda.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def declared_symbols() -> list[str]:
-    text = HEADER.read_text()
-    return re.findall(r"^MUSPACE_API\s+(?:const\s+)?\w+\s*\*?\s*(\w+)\s*\(", text, re.M)
+    names = []
+    for header in HEADERS:
+        names += re.findall(r"^MUSPACE_API\s+(?:const\s+)?\w+\s*\*?\s*(\w+)\s*\(",
+                            header.read_text(), re.M)
+    return names
 
 
 def test_header_declares_the_reference_entry_points():
     names = declared_symbols()
     assert {"ms_deform_attn_forward", "ms_deform_attn_backward", "add_one",
-            "muspace_last_error", "muspace_abi_version"} <= set(names)
+            "muspace_last_error", "muspace_abi_version",
+            "deformable_aggregation_forward_opt", "deformable_aggregation_backward_opt",
+            "deformable_aggregation_forward_base", "deformable_aggregation_backward_base"} <= set(names)
 
 
 def test_library_exports_every_declared_symbol(native_lib):
