@@ -44,6 +44,8 @@ from muspace_amd.workloads import (  # noqa: E402
     HBM_PEAK_GBPS,
     algorithmic_bytes,
     make_inputs,
+    dfa_algorithmic_bytes,
+    make_dfa_inputs,
     make_sca_inputs,
     sca_algorithmic_bytes,
 )
@@ -224,6 +226,37 @@ def time_sca(lib, steps: int = 50, warmup: int = 10) -> dict:
     return res
 
 
+def time_dfa(lib, steps: int = 50, warmup: int = 10) -> dict:
+    """Deformable aggregation at SparseDrive's production shape, kernel-only
+    scope as the reference's benchmark
+    (/root/reference/benchmarks/deformable_aggregation/README.md:31-40): output
+    and gradients allocated once before the timed region, one entry-point call
+    per launch (the kernels add into those buffers, which changes the values,
+    not the work)."""
+    t = make_dfa_inputs(device="cuda")
+    mc, spatial, start = t["mc_ms_feat"], t["spatial_shape"], t["scale_start_index"]
+    loc, weights, grad = t["sampling_location"], t["weights"], t["grad_output"]
+    out = torch.zeros((mc.shape[0], loc.shape[1], mc.shape[2]), device="cuda")
+    gf, gl, gw = torch.zeros_like(mc), torch.zeros_like(loc), torch.zeros_like(weights)
+    fwd_ms = _event_ms(lambda: lib.deformable_aggregation_forward_opt(
+        mc, spatial, start, loc, weights, out), steps, warmup)
+    bwd_ms = _event_ms(lambda: lib.deformable_aggregation_backward_opt(
+        mc, spatial, start, loc, weights, grad, gf, gl, gw), steps, warmup)
+    fwd_b, bwd_b = dfa_algorithmic_bytes()
+    active = float(((loc > 0) & (loc < 1)).all(-1).float().mean())
+    return {
+        "workload": "SparseDrive deformable aggregation: mc_ms_feat [8, 89760, 256], 6 cameras x "
+                    "4 scales, 900 anchors x 13 points, 8 groups, float32, "
+                    f"active fraction {active:.4f}",
+        "fwd_us": round(fwd_ms * 1e3, 1),
+        "bwd_us": round(bwd_ms * 1e3, 1),
+        "fwd_GBps": round(fwd_b / (fwd_ms * 1e-3) / 1e9, 1),
+        "bwd_GBps": round(bwd_b / (bwd_ms * 1e-3) / 1e9, 1),
+        "algorithmic_bytes": {"fwd": fwd_b, "bwd": bwd_b},
+        "published_ms": {"MTT S5000 fwd": 7.7067, "MTT S5000 bwd": 25.1164},
+    }
+
+
 def cpu_baseline(cfg, queries: int) -> dict:
     """The oracle (CPU restatement of the reference's PyTorch path) on a query subset."""
     from oracle import msda_torch
@@ -279,6 +312,8 @@ def main() -> int:
     parser.add_argument("--cpu-queries", type=int, default=500)
     parser.add_argument("--sca-only", action="store_true",
                         help="only the fused spatial cross-attention scatter-average leg")
+    parser.add_argument("--dfa-only", action="store_true",
+                        help="only the deformable aggregation leg")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="only run a device-to-device copy of this many MiB, 5 times "
                              "(calibrates the FETCH_SIZE / WRITE_SIZE counters), then exit")
@@ -308,6 +343,9 @@ def main() -> int:
     lib = load_native_module()
     if args.sca_only:
         print(json.dumps({"sca-scatter-div-float32": time_sca(lib, args.steps, args.warmup)}))
+        return 0
+    if args.dfa_only:
+        print(json.dumps({"sparsedrive-dfa-float32": time_dfa(lib, args.steps, args.warmup)}))
         return 0
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
@@ -341,6 +379,9 @@ def main() -> int:
         extra["bevformer-1l-published_ms"] = {"MTT S5000": 4.2387, "A100 (mmcv CUDA)": 4.0895}
         print("[bench] extra sca-scatter-div", file=sys.stderr, flush=True)
         extra["sca-scatter-div-float32"] = time_sca(lib)
+        torch.cuda.empty_cache()
+        print("[bench] extra sparsedrive-dfa", file=sys.stderr, flush=True)
+        extra["sparsedrive-dfa-float32"] = time_dfa(lib)
         torch.cuda.empty_cache()
 
     cpu = None

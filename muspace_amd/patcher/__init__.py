@@ -1,12 +1,14 @@
-"""Runtime patchers (the MSDA part of /root/reference/mu_space/patcher)."""
+"""Runtime patchers (the MSDA and deformable-aggregation parts of /root/reference/mu_space/patcher)."""
 
 from .runtime import (
     DefaultPatcher,
     PatchError,
     PatchReport,
     QwenDrivePatcher,
+    SparseDrivePatcher,
     default_patcher,
     qwendrive_patcher,
+    sparsedrive_patcher,
 )
 
 __all__ = [
@@ -14,6 +16,8 @@ __all__ = [
     "PatchError",
     "PatchReport",
     "QwenDrivePatcher",
+    "SparseDrivePatcher",
     "default_patcher",
     "qwendrive_patcher",
+    "sparsedrive_patcher",
 ]

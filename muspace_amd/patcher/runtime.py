@@ -46,6 +46,13 @@ QWENDRIVE_ATTENTION_MODULE = "qwen_drive_perception.attention"
 QWENDRIVE_MSDA_ATTR = "multi_scale_deformable_attn_cuda"
 QWENDRIVE_OPS_MODULE = "qwen_drive_perception.ops"
 QWENDRIVE_MSDA_FORWARD_ATTR = "ms_deform_attn_bf16_forward"
+# SparseDrive's deformable aggregation entry (reference runtime.py:61-66)
+SPARSEDRIVE_OPS_MODULE = "projects.mmdet3d_plugin.ops"
+SPARSEDRIVE_DAF_ATTR = "deformable_aggregation_function"
+SPARSEDRIVE_IMPORTED_MODULES = ("projects.mmdet3d_plugin.models.blocks",)
+SPARSEDRIVE_IMPORTED_ATTR = "DAF"
+SPARSEDRIVE_PACKAGE = "projects"
+SPARSEDRIVE_DAF_VALID_ATTR = "DAF_VALID"
 
 _SAVED_LOAD_EXT = "_muspace_original_load_ext"
 
@@ -377,14 +384,97 @@ class QwenDrivePatcher:
         )
 
 
+def _make_deformable_aggregation_wrapper(strict: bool) -> PatchCallable:
+    """SparseDrive's ``deformable_aggregation_function`` signature (reference
+    runtime.py:519-545): strict forces the HIP backend, otherwise ``auto``."""
+    backend = "hip" if strict else "auto"
+
+    def muspace_deformable_aggregation(feature_maps, spatial_shape, scale_start_index,
+                                       sampling_location, weights):
+        from ..ops.deformable_aggregation import deformable_aggregation_function
+
+        return deformable_aggregation_function(feature_maps, spatial_shape, scale_start_index,
+                                               sampling_location, weights, backend=backend)
+
+    muspace_deformable_aggregation.__name__ = (
+        "muspace_deformable_aggregation_strict" if strict else "muspace_deformable_aggregation"
+    )
+    muspace_deformable_aggregation.__module__ = __name__
+    return muspace_deformable_aggregation
+
+
+class SparseDrivePatcher:
+    """Route SparseDrive's deformable aggregation to this operator.
+
+    Rebinds ``projects.mmdet3d_plugin.ops.deformable_aggregation_function``,
+    the ``DAF`` copy already imported by ``models.blocks``, and sets
+    ``DAF_VALID = True`` where the checkout cached a failed extension probe
+    (reference ``SparseDrivePatcher._patch_sparsedrive_daf``,
+    runtime.py:1471-1510). The reference patcher's flash-attention and CUDA-shim
+    replacements are outside this operator and not installed.
+    """
+
+    def __init__(self) -> None:
+        self._originals: dict[tuple[str, str], object] = {}
+        self._strict: bool | None = None
+
+    def apply(self, *, strict: bool | None = None) -> PatchReport:
+        strict = _env_strict() if strict is None else strict
+        try:
+            ops = importlib.import_module(SPARSEDRIVE_OPS_MODULE)
+        except ImportError as exc:
+            raise PatchError(
+                "SparseDrive ops package import failed. Ensure the SparseDrive checkout is "
+                "on PYTHONPATH before sparsedrive_patcher.apply()."
+            ) from exc
+        if not hasattr(ops, SPARSEDRIVE_DAF_ATTR):
+            raise PatchError(f"{SPARSEDRIVE_OPS_MODULE}.{SPARSEDRIVE_DAF_ATTR} is unavailable")
+        wrapper = _make_deformable_aggregation_wrapper(strict)
+        _patch_attr(self._originals, ops, SPARSEDRIVE_DAF_ATTR, wrapper)
+        patched = [ops.__name__]
+        for name in SPARSEDRIVE_IMPORTED_MODULES:
+            module = sys.modules.get(name)
+            if module is not None and _patch_attr(self._originals, module,
+                                                  SPARSEDRIVE_IMPORTED_ATTR, wrapper):
+                patched.append(name)
+        prefix = f"{SPARSEDRIVE_PACKAGE}."
+        for name, module in list(sys.modules.items()):
+            if module is None or not (name == SPARSEDRIVE_PACKAGE or name.startswith(prefix)):
+                continue
+            if getattr(module, SPARSEDRIVE_DAF_VALID_ATTR, None) is False:
+                _patch_attr(self._originals, module, SPARSEDRIVE_DAF_VALID_ATTR, True)
+                patched.append(name)
+        action = "already-applied" if self._strict == strict else "applied"
+        self._strict = strict
+        return PatchReport(
+            target=f"{SPARSEDRIVE_OPS_MODULE}.{SPARSEDRIVE_DAF_ATTR}",
+            strict=strict,
+            action=action,
+            patched_modules=tuple(dict.fromkeys(patched)),
+        )
+
+    def restore(self) -> PatchReport:
+        restored = _restore_attrs(self._originals)
+        self._strict = None
+        return PatchReport(
+            target=f"{SPARSEDRIVE_OPS_MODULE}.{SPARSEDRIVE_DAF_ATTR}",
+            strict=False,
+            action="restored",
+            patched_modules=tuple(restored),
+        )
+
+
 default_patcher = DefaultPatcher()
 qwendrive_patcher = QwenDrivePatcher()
+sparsedrive_patcher = SparseDrivePatcher()
 
 __all__ = [
     "DefaultPatcher",
     "PatchError",
     "PatchReport",
     "QwenDrivePatcher",
+    "SparseDrivePatcher",
     "default_patcher",
     "qwendrive_patcher",
+    "sparsedrive_patcher",
 ]

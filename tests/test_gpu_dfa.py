@@ -134,3 +134,24 @@ def test_production_shape_matches_the_oracle():
     expected.backward(grad_out)
     for a, e in zip((native[0], native[3], native[4]), (oracle_in[0], oracle_in[3], oracle_in[4])):
         torch.testing.assert_close(a.grad, e.grad, rtol=1e-4, atol=1e-4)
+
+
+def test_sparsedrive_patched_entry_runs_the_hip_kernels(monkeypatch):
+    import sys
+    import types
+
+    from muspace_amd.patcher import SparseDrivePatcher
+
+    ops = types.ModuleType("projects.mmdet3d_plugin.ops")
+    ops.deformable_aggregation_function = lambda *a: None
+    monkeypatch.setitem(sys.modules, ops.__name__, ops)
+    patcher = SparseDrivePatcher()
+    patcher.apply(strict=True)
+    try:
+        clear_dispatch_report()
+        mc, spatial, start, loc, weights = _to_device(small_case(), requires_grad=False)
+        out = ops.deformable_aggregation_function(mc, spatial.long(), start.long(), loc, weights)
+        assert get_last_dispatch_report().selected_backend == "hip"
+        torch.testing.assert_close(out.cpu(), SMALL_EXPECTED, rtol=1e-5, atol=1e-5)
+    finally:
+        patcher.restore()

@@ -215,3 +215,57 @@ def test_qwendrive_missing_symbols_is_a_patch_error(monkeypatch):
     monkeypatch.delattr(attention, "multi_scale_deformable_attn_cuda")
     with pytest.raises(PatchError, match="missing the symbols"):
         QwenDrivePatcher().apply()
+
+
+# ------------------------------------------------------------ SparseDrive ---
+
+
+def test_sparsedrive_patcher(monkeypatch):
+    """Reference tests/ops/test_deformable_aggregation.py:112-131."""
+    from muspace_amd.patcher import SparseDrivePatcher
+
+    ops = types.ModuleType("projects.mmdet3d_plugin.ops")
+    blocks = types.ModuleType("projects.mmdet3d_plugin.models.blocks")
+
+    def original(*args, **kwargs):
+        return "original"
+
+    ops.deformable_aggregation_function = original
+    blocks.DAF = original
+    blocks.DAF_VALID = False
+    monkeypatch.setitem(sys.modules, ops.__name__, ops)
+    monkeypatch.setitem(sys.modules, blocks.__name__, blocks)
+
+    patcher = SparseDrivePatcher()
+    report = patcher.apply()
+    assert report.action == "applied"
+    assert ops.deformable_aggregation_function is not original
+    assert blocks.DAF is ops.deformable_aggregation_function
+    assert blocks.DAF_VALID is True
+    assert ops.deformable_aggregation_function.__name__ == "muspace_deformable_aggregation"
+    assert patcher.restore().action == "restored"
+    assert ops.deformable_aggregation_function is original and blocks.DAF is original
+    assert blocks.DAF_VALID is False
+
+
+def test_sparsedrive_patched_entry_computes_on_the_cpu(monkeypatch):
+    from muspace_amd.patcher import SparseDrivePatcher
+    from test_dfa_oracle import SMALL_EXPECTED, small_case
+
+    ops = types.ModuleType("projects.mmdet3d_plugin.ops")
+    ops.deformable_aggregation_function = lambda *a: None
+    monkeypatch.setitem(sys.modules, ops.__name__, ops)
+    patcher = SparseDrivePatcher()
+    patcher.apply()
+    mc, spatial, start, loc, weights = small_case()
+    out = ops.deformable_aggregation_function(mc, spatial.long(), start.long(), loc, weights)
+    torch.testing.assert_close(out, SMALL_EXPECTED)
+    patcher.restore()
+
+
+def test_sparsedrive_missing_ops_module_is_a_patch_error(monkeypatch):
+    from muspace_amd.patcher import SparseDrivePatcher
+
+    monkeypatch.setitem(sys.modules, "projects.mmdet3d_plugin.ops", None)
+    with pytest.raises(PatchError, match="SparseDrive ops package import failed"):
+        SparseDrivePatcher().apply()
