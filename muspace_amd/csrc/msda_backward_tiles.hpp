@@ -242,8 +242,8 @@ __global__ void __launch_bounds__(kBinBlock)
       live[u] = i < total && smp[u] < s.lp;
       const size_t o =
           live[u] ? (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp[u] : 0;
-      lx[u] = to_float(loc[2 * o]);
-      ly[u] = to_float(loc[2 * o + 1]);
+      lx[u] = load_nt(&loc[2 * o]);
+      ly[u] = load_nt(&loc[2 * o + 1]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -743,7 +743,7 @@ __global__ void __launch_bounds__(kTileBlock)
     batch_range(c, s0, s1);
     const uint32_t i = s0 + tid + u * kTileBlock;
     const size_t at = c.valid && i < s1 ? rec_base(c.d) + i : 0;
-    return records[at];
+    return load_nt(records + at);  // each record is read once
   };
   auto slab_offset = [&](const Item &d) {
     return static_cast<size_t>(d.b) * s.spatial * MC + d.m * C;
@@ -805,7 +805,8 @@ __global__ void __launch_bounds__(kTileBlock)
       }
       float *dst = grad_value + slab + static_cast<size_t>(Lw.start + y * Lw.w + x) * MC + ch;
       if (!split && r < T && c < T && !boundary_cell(r, c, g)) {
-        *reinterpret_cast<float4 *>(dst) = sum;
+        const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
+        store16_nt(dst, sv);
       } else {
         unsafeAtomicAdd(dst, sum.x);
         unsafeAtomicAdd(dst + 1, sum.y);
@@ -1088,8 +1089,8 @@ __global__ void __launch_bounds__(kTileBlock)
         const float ga = wy0 * (wx0 * D0 + wx1 * D1) + wy1 * (wx0 * D2 + wx1 * D3);
         const float gx = a * (wy0 * (D1 - D0) + wy1 * (D3 - D2)) * L.fw;
         const float gy = a * (wx0 * (D2 - D0) + wx1 * (D3 - D1)) * L.fh;
-        records[rb + i] =
-            make_uint4(__float_as_uint(ga), __float_as_uint(gx), __float_as_uint(gy), 0u);
+        store_nt(records + rb + i,
+                 make_uint4(__float_as_uint(ga), __float_as_uint(gx), __float_as_uint(gy), 0u));
       }
     }
     if (tid < NPOS) pcount[tid] = 0;

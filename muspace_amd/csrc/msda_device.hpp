@@ -146,6 +146,49 @@ __device__ __forceinline__ void store16(T *p, const float (&v)[8]) {
   *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Streaming accesses: data read or written once per launch is marked
+// non-temporal, so that it does not displace the lines a kernel reuses (the
+// gathered value rows) from L2. Measured at c2: forward 424 -> 381 us;
+// backward 884 -> 865 us (tile records, results and write-back; bin_count's
+// locations). bin_scatter's and grad_gather's streams measured slower marked
+// and are left as they are.
+typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float load_nt(const float *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ float load_nt(const bf16_t *p) {
+  const unsigned short b = __builtin_nontemporal_load(reinterpret_cast<const unsigned short *>(p));
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ float load_nt(const __half *p) {
+  const unsigned short b = __builtin_nontemporal_load(reinterpret_cast<const unsigned short *>(p));
+  return __half2float(__ushort_as_half(b));
+}
+
+__device__ __forceinline__ uint4 load_nt(const uint4 *p) {
+  const nt_u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4 *>(p));
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+__device__ __forceinline__ void store_nt(uint4 *p, const uint4 v) {
+  const nt_u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<nt_u32x4 *>(p));
+}
+
+__device__ __forceinline__ void store16_nt(float *p, const float (&v)[4]) {
+  const nt_u32x4 w = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                      __float_as_uint(v[3])};
+  __builtin_nontemporal_store(w, reinterpret_cast<nt_u32x4 *>(p));
+}
+template <typename T>
+__device__ __forceinline__ void store16_nt(T *p, const float (&v)[8]) {
+  nt_u32x4 w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i] = static_cast<uint32_t>(bits16(from_float<T>(v[2 * i]))) |
+           (static_cast<uint32_t>(bits16(from_float<T>(v[2 * i + 1]))) << 16);
+  }
+  __builtin_nontemporal_store(w, reinterpret_cast<nt_u32x4 *>(p));
+}
+
 // ------------------------------------------------------- cross-lane sums ---
 
 #define MSDA_DPP(v, ctrl)                                                            \

@@ -100,7 +100,7 @@ struct DenseRows {
   template <int C, int CPL>
   __device__ __forceinline__ void put(int b, int q, int m, int k, const float (&acc)[CPL],
                                       const Ticket &, const Shape &s) const {
-    store16(out + static_cast<size_t>((b * s.queries + q) * s.heads + m) * C + k * CPL, acc);
+    store16_nt(out + static_cast<size_t>((b * s.queries + q) * s.heads + m) * C + k * CPL, acc);
   }
   __device__ __forceinline__ void put1(int b, int q, int m, int c, float acc,
                                        const Shape &s) const {
@@ -310,9 +310,9 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
     size_t slab = 0;
     if (live) out.locate(tu.b, tu.q, tu.m, s, grow, slab);
     const size_t o = static_cast<size_t>(grow) * s.lp + sm;
-    lx = to_float(loc[2 * o]);
-    ly = to_float(loc[2 * o + 1]);
-    a = to_float(attn[o]);
+    lx = load_nt(&loc[2 * o]);  // geometry streams through once
+    ly = load_nt(&loc[2 * o + 1]);
+    a = load_nt(&attn[o]);
     unit_base = static_cast<uint32_t>((slab * MC + tu.m * C) * VB);
   };
   load_geometry(0);
