@@ -772,8 +772,10 @@ __global__ void __launch_bounds__(kTileBlock)
                 : kOobOffset;
         unsigned char *dst = reinterpret_cast<unsigned char *>(vt) +
                              static_cast<size_t>(wave * kWave + v * kTileBlock) * 16;
+        // cache policy 2 = non-temporal: a tile's value rows are staged once
+        // (c1 and c3 backward 1-3% faster, c2 unchanged)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            vrsrc, (__attribute__((address_space(3))) void *)dst, 16, off, 0, 0, 0);
+            vrsrc, (__attribute__((address_space(3))) void *)dst, 16, off, 0, 0, 2);
       }
     }
   };
