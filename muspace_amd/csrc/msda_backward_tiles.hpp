@@ -69,6 +69,11 @@ struct BinPlan {
   int rmax;         // records per work item (a multiple of the batch size)
   int item_cap;     // capacity of the compact work-item list (all slabs)
   int64_t rec_cap;  // records per slab = queries * lp (one per sample)
+  // 1: the tile kernel writes each record's location and weight gradients
+  // straight to the sample's place (and bin_scatter zeroes samples without a
+  // record); 0: it stores them over the record and msda_grad_gather copies
+  // them into sample order through rec_of_sample.
+  int direct;
 };
 
 // One work item: records [r0, r1) of one tile of the (b, m) slab. `tile`
@@ -418,6 +423,7 @@ __global__ void __launch_bounds__(kBinBlock)
                      const GT *__restrict__ loc, const GT *__restrict__ attn, Shape s, BinPlan p,
                      const uint32_t *__restrict__ counts, const uint32_t *__restrict__ zero_tiles,
                      uint4 *__restrict__ records, uint32_t *__restrict__ rec_of_sample,
+                     float *__restrict__ grad_loc, float *__restrict__ grad_attn,
                      float *__restrict__ grad_value) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
@@ -490,7 +496,13 @@ __global__ void __launch_bounds__(kBinBlock)
         rk[u] = rank;
       }
       if (live) {
-        rec_of_sample[(static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp] = at;
+        const size_t o = (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp;
+        if (!p.direct) {
+          rec_of_sample[o] = at;
+        } else if (at == kNoRecord) {  // no record: its gradients are zero
+          grad_attn[o] = 0.0f;
+          *reinterpret_cast<float2 *>(grad_loc + 2 * o) = make_float2(0.0f, 0.0f);
+        }
       }
     }
     lds_barrier();
@@ -627,7 +639,8 @@ __global__ void __launch_bounds__(kTileBlock)
                        const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                        const VT *__restrict__ grad_out, uint4 *__restrict__ records,
                        const Item *__restrict__ items, uint32_t *__restrict__ item_total,
-                       Shape s, BinPlan p, float *__restrict__ grad_value) {
+                       Shape s, BinPlan p, float *__restrict__ grad_value,
+                       float *__restrict__ grad_loc, float *__restrict__ grad_attn) {
   using Cfg = TileCfg<VT, C>;
   constexpr int T = Cfg::T, K = Cfg::K, CPL = Cfg::CPL;
   constexpr int TV = T + 1, NPOS = TV * TV;
@@ -857,9 +870,11 @@ __global__ void __launch_bounds__(kTileBlock)
     int pos[RPT];
     uint32_t rank[RPT];
     float my_wx1[RPT], my_wy1[RPT], my_a[RPT];
+    uint32_t my_id[RPT];  // query << lp_log2 | sample
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
       const int i = tid + u * kTileBlock;
+      my_id[u] = r_cur[u].x & kSampleMask;
       pos[u] = -1;
       rank[u] = 0;
       my_wx1[u] = my_wy1[u] = 0.0f;
@@ -1079,6 +1094,7 @@ __global__ void __launch_bounds__(kTileBlock)
       asm volatile("" : "+v"(r_cur[u].x), "+v"(r_cur[u].y), "+v"(r_cur[u].z), "+v"(r_cur[u].w));
     }
     const size_t rb = rec_base(c0.d) + s0;
+    const size_t sb = (static_cast<size_t>(c0.d.b) * s.queries * s.heads + c0.d.m) * s.lp;
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
       const int i = tid + u * kTileBlock;
@@ -1091,8 +1107,15 @@ __global__ void __launch_bounds__(kTileBlock)
         const float ga = wy0 * (wx0 * D0 + wx1 * D1) + wy1 * (wx0 * D2 + wx1 * D3);
         const float gx = a * (wy0 * (D1 - D0) + wy1 * (D3 - D2)) * L.fw;
         const float gy = a * (wx0 * (D2 - D0) + wx1 * (D3 - D1)) * L.fh;
-        store_nt(records + rb + i,
-                 make_uint4(__float_as_uint(ga), __float_as_uint(gx), __float_as_uint(gy), 0u));
+        if (p.direct) {  // straight to the sample's place: o = ((b*Q + q)*M + m)*lp + smp
+          const uint32_t q = my_id[u] >> p.lp_log2, smp = my_id[u] & ((1u << p.lp_log2) - 1u);
+          const size_t o = sb + static_cast<size_t>(q) * s.heads * s.lp + smp;
+          grad_attn[o] = ga;
+          *reinterpret_cast<float2 *>(grad_loc + 2 * o) = make_float2(gx, gy);
+        } else {
+          store_nt(records + rb + i, make_uint4(__float_as_uint(ga), __float_as_uint(gx),
+                                                __float_as_uint(gy), 0u));
+        }
       }
     }
     if (tid < NPOS) pcount[tid] = 0;
