@@ -119,6 +119,35 @@ MUSPACE_API int ms_deform_attn_backward_ws(
     int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
     size_t workspace_bytes, void *stream);
 
+/* ms_deform_attn_backward_ws in two calls on the same workspace and the same
+ * arguments: _bin runs the binning of the tile-owned path (it reads only the
+ * geometry -- sampling_locations, attention_weights and the level metadata --
+ * and already writes parts of the three gradient buffers), _rest the rest
+ * (it reads value and grad_output). _bin may therefore be issued before
+ * grad_output exists, e.g. on a second stream during the forward; the caller
+ * orders _rest after it (same stream or an event), keeps the workspace and the
+ * gradient buffers alive in between and passes identical arguments to both,
+ * except that grad_output may be NULL in _bin. Each _bin serves one _rest
+ * (the rest consumes the binned work list). Shapes the tile path does not
+ * take do nothing in _bin and everything in _rest. No reference counterpart
+ * (the reference backward is one launch). */
+MUSPACE_API int ms_deform_attn_backward_bin(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_weights, int geometry_dtype, const void *grad_output,
+    float *grad_value, float *grad_sampling_locations, float *grad_attention_weights,
+    int64_t batch, int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream);
+MUSPACE_API int ms_deform_attn_backward_rest(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_weights, int geometry_dtype, const void *grad_output,
+    float *grad_value, float *grad_sampling_locations, float *grad_attention_weights,
+    int64_t batch, int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream);
+
 /* BEVFormer spatial cross-attention, one camera, with the scatter-average
  * fused into the forward: for the camera-rebatched
  *   value               [batch*num_cams, spatial_size, num_heads, channels]  value_dtype

@@ -578,11 +578,16 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   return true;
 }
 
+// Parts of the backward: binning (bin_count, bin_scan, bin_scatter) reads only
+// the geometry and may run before grad_output exists, e.g. on a second stream
+// during the forward; the rest needs grad_output and the binned workspace.
+enum class Phase { kAll, kBin, kRest };
+
 template <typename VT, typename GT, int C>
 void launch_backward_tiles(const void *value, const int64_t *shapes, const int64_t *starts,
                            const void *loc, const void *attn, const void *grad_out, float *gv,
                            float *gl, float *ga, const msda::Shape &s, const TileWorkspace &w,
-                           void *workspace, hipStream_t st) {
+                           void *workspace, Phase phase, hipStream_t st) {
   constexpr int T = msda::TileCfg<VT, C>::T;
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + w.counts);
@@ -612,12 +617,15 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(tile),
                             hipFuncAttributeMaxDynamicSharedMemorySize, tile_bytes);
 
-  count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts,
-                                                             item_total, gv);
-  msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
-      shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
-  scatter<<<bm * p.chunks, msda::kBinBlock, scatter_bytes, st>>>(
-      shapes, starts, lc, aw, s, p, counts, zero_tiles, records, rec_of_sample, gl, ga, gv);
+  if (phase != Phase::kRest) {
+    count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts,
+                                                               item_total, gv);
+    msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
+        shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
+    scatter<<<bm * p.chunks, msda::kBinBlock, scatter_bytes, st>>>(
+        shapes, starts, lc, aw, s, p, counts, zero_tiles, records, rec_of_sample, gl, ga, gv);
+  }
+  if (phase == Phase::kBin) return;
   const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
   tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, vbytes, shapes, starts, go, records, items,
                                                           item_total, s, p, gv, gl, ga);
@@ -632,29 +640,32 @@ template <typename VT, typename GT>
 void launch_backward(const void *value, const int64_t *shapes, const int64_t *starts,
                      const void *loc, const void *attn, const void *grad_out, float *gv,
                      float *gl, float *ga, const msda::Shape &s, void *workspace,
-                     size_t workspace_bytes, hipStream_t st) {
+                     size_t workspace_bytes, Phase phase, hipStream_t st) {
   constexpr int value_dtype = std::is_same<VT, float>::value ? MUSPACE_DTYPE_F32
                                                              : MUSPACE_DTYPE_F16;
   TileWorkspace w;
   const bool tiles = plan_tile_workspace(s, value_dtype, w) && workspace != nullptr &&
                      workspace_bytes >= w.bytes && rows_aligned({value, grad_out, gv}, gl) &&
                      aligned(workspace, 256);
-  if (!tiles) {
-    launch_backward_atomic<VT, GT>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga, s, st);
+  if (!tiles) {  // the atomic fallback has no binning: all of it is the second part
+    if (phase != Phase::kBin) {
+      launch_backward_atomic<VT, GT>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga, s,
+                                     st);
+    }
     return;
   }
   switch (s.channels) {
     case 16:
       launch_backward_tiles<VT, GT, 16>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga,
-                                        s, w, workspace, st);
+                                        s, w, workspace, phase, st);
       return;
     case 32:
       launch_backward_tiles<VT, GT, 32>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga,
-                                        s, w, workspace, st);
+                                        s, w, workspace, phase, st);
       return;
     default:
       launch_backward_tiles<VT, GT, 64>(value, shapes, starts, loc, attn, grad_out, gv, gl, ga,
-                                        s, w, workspace, st);
+                                        s, w, workspace, phase, st);
       return;
   }
 }
@@ -664,60 +675,32 @@ int backward_impl(const char *fn, const void *value, int value_dtype,
                   const void *sampling_locations, const void *attention_weights,
                   int geometry_dtype, const void *grad_output, float *grad_value,
                   float *grad_sampling_locations, float *grad_attention_weights, const Args &a,
-                  void *workspace, size_t workspace_bytes, hipStream_t st) {
+                  void *workspace, size_t workspace_bytes, hipStream_t st,
+                  Phase phase = Phase::kAll) {
   msda::Shape s;
   if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
   const int64_t nvalue = a.batch * a.spatial * a.heads * a.channels;
   if (nvalue > 0 && !grad_value) return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
   if (!needs_data(s) || s.lp == 0) {
     // nothing samples the value: its gradient is zero
-    if (nvalue > 0) {
+    if (nvalue > 0 && phase != Phase::kBin) {
       msda::zero_kernel<<<generic_blocks(nvalue), msda::kBlock, 0, st>>>(grad_value, nvalue);
       return check_launch(fn);
     }
     return ok();
   }
+  // the binning part does not read grad_output, which may not exist yet
   if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
-      !attention_weights || !grad_output || !grad_sampling_locations || !grad_attention_weights) {
+      !attention_weights || (!grad_output && phase != Phase::kBin) || !grad_sampling_locations ||
+      !grad_attention_weights) {
     return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
   }
-  using msda::bf16_t;
-  switch (value_dtype) {
-    case MUSPACE_DTYPE_F32:
-      launch_backward<float, float>(value, spatial_shapes, level_start_index, sampling_locations,
-                                    attention_weights, grad_output, grad_value,
-                                    grad_sampling_locations, grad_attention_weights, s,
-                                    workspace, workspace_bytes, st);
-      break;
-    case MUSPACE_DTYPE_F16:
-      if (geometry_dtype == MUSPACE_DTYPE_F32) {
-        launch_backward<__half, float>(value, spatial_shapes, level_start_index,
-                                       sampling_locations, attention_weights, grad_output,
-                                       grad_value, grad_sampling_locations,
-                                       grad_attention_weights, s, workspace, workspace_bytes, st);
-      } else {
-        launch_backward<__half, __half>(value, spatial_shapes, level_start_index,
-                                        sampling_locations, attention_weights, grad_output,
-                                        grad_value, grad_sampling_locations,
-                                        grad_attention_weights, s, workspace, workspace_bytes,
-                                        st);
-      }
-      break;
-    default:
-      if (geometry_dtype == MUSPACE_DTYPE_F32) {
-        launch_backward<bf16_t, float>(value, spatial_shapes, level_start_index,
-                                       sampling_locations, attention_weights, grad_output,
-                                       grad_value, grad_sampling_locations,
-                                       grad_attention_weights, s, workspace, workspace_bytes, st);
-      } else {
-        launch_backward<bf16_t, bf16_t>(value, spatial_shapes, level_start_index,
-                                        sampling_locations, attention_weights, grad_output,
-                                        grad_value, grad_sampling_locations,
-                                        grad_attention_weights, s, workspace, workspace_bytes,
-                                        st);
-      }
-      break;
-  }
+  with_dtypes(value_dtype, geometry_dtype, [&](auto vt, auto gt) {
+    launch_backward<decltype(vt), decltype(gt)>(
+        value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+        grad_output, grad_value, grad_sampling_locations, grad_attention_weights, s, workspace,
+        workspace_bytes, phase, st);
+  });
   return check_launch(fn);
 }
 
@@ -956,6 +939,42 @@ int ms_deform_attn_backward_ws(const void *value, int value_dtype, const int64_t
                        level_start_index, sampling_locations, attention_weights, geometry_dtype,
                        grad_output, grad_value, grad_sampling_locations, grad_attention_weights,
                        a, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int ms_deform_attn_backward_bin(const void *value, int value_dtype,
+                                const int64_t *spatial_shapes, const int64_t *level_start_index,
+                                const void *sampling_locations, const void *attention_weights,
+                                int geometry_dtype, const void *grad_output, float *grad_value,
+                                float *grad_sampling_locations, float *grad_attention_weights,
+                                int64_t batch, int64_t spatial_size, int64_t num_heads,
+                                int64_t channels, int64_t num_levels, int64_t num_query,
+                                int64_t num_point, int64_t im2col_step, void *workspace,
+                                size_t workspace_bytes, void *stream) {
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  return backward_impl("ms_deform_attn_backward_bin", value, value_dtype, spatial_shapes,
+                       level_start_index, sampling_locations, attention_weights, geometry_dtype,
+                       grad_output, grad_value, grad_sampling_locations, grad_attention_weights,
+                       a, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                       Phase::kBin);
+}
+
+int ms_deform_attn_backward_rest(const void *value, int value_dtype,
+                                 const int64_t *spatial_shapes, const int64_t *level_start_index,
+                                 const void *sampling_locations, const void *attention_weights,
+                                 int geometry_dtype, const void *grad_output, float *grad_value,
+                                 float *grad_sampling_locations, float *grad_attention_weights,
+                                 int64_t batch, int64_t spatial_size, int64_t num_heads,
+                                 int64_t channels, int64_t num_levels, int64_t num_query,
+                                 int64_t num_point, int64_t im2col_step, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  return backward_impl("ms_deform_attn_backward_rest", value, value_dtype, spatial_shapes,
+                       level_start_index, sampling_locations, attention_weights, geometry_dtype,
+                       grad_output, grad_value, grad_sampling_locations, grad_attention_weights,
+                       a, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                       Phase::kRest);
 }
 
 int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *spatial_shapes,

@@ -57,6 +57,18 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         + [_c_ptr, ctypes.c_size_t, _c_ptr],
     ),
     "ms_deform_attn_backward_workspace_size": (ctypes.c_size_t, [_c_int] + [_c_int64] * 7),
+    "ms_deform_attn_backward_bin": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "ms_deform_attn_backward_rest": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
     "ms_deform_attn_forward_scatter_div": (
         _c_int,
         [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr]
@@ -139,6 +151,9 @@ class NativeLibrary:
         self._bound: dict[str, Callable[..., Any]] = {
             "ms_deform_attn_forward": self.ms_deform_attn_forward,
             "ms_deform_attn_backward": self.ms_deform_attn_backward,
+            "backward_workspace": self.backward_workspace,
+            "ms_deform_attn_backward_bin": self.ms_deform_attn_backward_bin,
+            "ms_deform_attn_backward_rest": self.ms_deform_attn_backward_rest,
             "ms_deform_attn_forward_scatter_div": self.ms_deform_attn_forward_scatter_div,
             "ms_deform_attn_forward_scatter_div_cams": self.ms_deform_attn_forward_scatter_div_cams,
             "deformable_aggregation_forward_opt": self.deformable_aggregation_forward_opt,
@@ -257,21 +272,77 @@ class NativeLibrary:
                      tuple(sampling_locations.shape))
         _check_shape(grad_attention_weights, "grad_attention_weights",
                      tuple(attention_weights.shape))
+        with torch.cuda.device(value.device):
+            workspace = self.backward_workspace(value, sampling_locations)
+            self._backward_call("ms_deform_attn_backward_ws", value, spatial_shapes,
+                                level_start_index, sampling_locations, attention_weights,
+                                grad_output, grad_value, grad_sampling_locations,
+                                grad_attention_weights, im2col_step, workspace,
+                                self._stream(value))
+
+    def backward_workspace(self, value, sampling_locations):
+        """Scratch of the tile-owned backward for these shapes (1 byte when the
+        shape takes the atomic fallback)."""
+        import torch
+
+        batch, spatial, heads, channels = value.shape
+        queries, levels, points = (sampling_locations.shape[1], sampling_locations.shape[3],
+                                   sampling_locations.shape[4])
         nbytes = self._raw["ms_deform_attn_backward_workspace_size"](
             _dtype_code(value.dtype), batch, spatial, heads, channels, levels, queries, points
         )
+        return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=value.device)
+
+    def _backward_call(self, name, value, spatial_shapes, level_start_index, sampling_locations,
+                       attention_weights, grad_output, grad_value, grad_sampling_locations,
+                       grad_attention_weights, im2col_step, workspace, stream) -> None:
+        batch, spatial, heads, channels = value.shape
+        levels = spatial_shapes.shape[0]
+        queries, points = sampling_locations.shape[1], sampling_locations.shape[4]
+        rc = self._raw[name](
+            value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
+            level_start_index.data_ptr(), sampling_locations.data_ptr(),
+            attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
+            None if grad_output is None else grad_output.data_ptr(), grad_value.data_ptr(),
+            grad_sampling_locations.data_ptr(), grad_attention_weights.data_ptr(),
+            batch, spatial, heads, channels, levels, queries, points,
+            int(im2col_step), workspace.data_ptr(), workspace.numel(), stream,
+        )
+        self._raise_on(rc, name)
+
+    def ms_deform_attn_backward_bin(
+        self, value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+        grad_value, grad_sampling_locations, grad_attention_weights, im2col_step, workspace,
+        stream=None,
+    ) -> None:
+        """First part of the backward (binning; geometry only) on ``stream``
+        (default: the current stream). Inputs were checked by the caller, which
+        passes the same tensors to :meth:`ms_deform_attn_backward_rest`."""
+        import torch
+
+        st = stream if stream is not None else torch.cuda.current_stream(value.device)
         with torch.cuda.device(value.device):
-            workspace = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=value.device)
-            rc = self._raw["ms_deform_attn_backward_ws"](
-                value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
-                level_start_index.data_ptr(), sampling_locations.data_ptr(),
-                attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
-                grad_output.data_ptr(), grad_value.data_ptr(),
-                grad_sampling_locations.data_ptr(), grad_attention_weights.data_ptr(),
-                batch, spatial, heads, channels, levels, queries, points,
-                int(im2col_step), workspace.data_ptr(), int(nbytes), self._stream(value),
-            )
-        self._raise_on(rc, "ms_deform_attn_backward")
+            self._backward_call("ms_deform_attn_backward_bin", value, spatial_shapes,
+                                level_start_index, sampling_locations, attention_weights, None,
+                                grad_value, grad_sampling_locations, grad_attention_weights,
+                                im2col_step, workspace, st.cuda_stream)
+
+    def ms_deform_attn_backward_rest(
+        self, value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+        grad_output, grad_value, grad_sampling_locations, grad_attention_weights, im2col_step,
+        workspace,
+    ) -> None:
+        """Second part of the backward on the current stream, after the binning
+        of the same workspace (ordered by the caller)."""
+        import torch
+
+        _check(grad_output, "grad", (value.dtype,))
+        with torch.cuda.device(value.device):
+            self._backward_call("ms_deform_attn_backward_rest", value, spatial_shapes,
+                                level_start_index, sampling_locations, attention_weights,
+                                grad_output, grad_value, grad_sampling_locations,
+                                grad_attention_weights, im2col_step, workspace,
+                                self._stream(value))
 
     def ms_deform_attn_forward_scatter_div(
         self, value, spatial_shapes, level_start_index, sampling_locations,

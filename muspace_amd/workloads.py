@@ -163,6 +163,18 @@ def algorithmic_bytes(
     return fwd, bwd
 
 
+def backward_rest_bytes(cfg: MSDAConfig, value_dtype: torch.dtype = torch.float32) -> int:
+    """Algorithmic bytes of the backward's second part (the tile kernel,
+    ms_deform_attn_backward_rest): the tensors it reads or writes, once --
+    value, grad_output and the three float32 gradients. Its binned records are
+    scratch derived from the locations and weights, which the binning read."""
+    vb = torch.empty((), dtype=value_dtype).element_size()
+    n_value = cfg.batch * cfg.spatial_size * cfg.heads * cfg.channels
+    n_attn = cfg.batch * cfg.queries * cfg.heads * cfg.num_levels * cfg.points
+    n_out = cfg.batch * cfg.queries * cfg.heads * cfg.channels
+    return n_value * vb + n_out * vb + 4 * (n_value + 2 * n_attn + n_attn)
+
+
 # ------------------------------------------------ spatial cross-attention ---
 
 SCA_BEV = (200, 200)  # BEVFormer-base BEV grid: 40000 queries

@@ -47,7 +47,8 @@ class _NativeCallSpy:
         target = getattr(self._inner, name)
 
         def recorded(*args, **kwargs):
-            self.calls.append((name, [getattr(arg, "dtype", None) for arg in args]))
+            if name != "backward_workspace":  # a size query, not a kernel entry point
+                self.calls.append((name, [getattr(arg, "dtype", None) for arg in args]))
             return target(*args, **kwargs)
 
         return recorded
@@ -112,6 +113,7 @@ def test_native_bf16_reaches_the_kernel_as_bfloat16(monkeypatch):
                        embed_dims=4, levels=((1, 2), (2, 1)), points=2)
     output = multi_scale_deformable_attn(*tensors, backend="hip")
     output.float().sum().backward()
+    # this shape (4 channels) takes the atomic backward: no early binning
     assert [name for name, _ in spy.calls] == ["ms_deform_attn_forward", "ms_deform_attn_backward"]
     assert spy.calls[0][1][:6] == [torch.bfloat16, torch.int64, torch.int64, torch.bfloat16,
                                    torch.bfloat16, torch.bfloat16]
@@ -184,3 +186,64 @@ def test_autograd_end_to_end_fp32_full_channel_layout():
     torch.testing.assert_close(out.detach().cpu(), expected.detach(), rtol=1e-5, atol=1e-5)
     for a, e in zip((value, loc, attn), (ref[0], ref[3], ref[4])):
         torch.testing.assert_close(a.grad.cpu(), e.grad, rtol=1e-4, atol=1e-4)
+
+
+def test_early_binning_matches_the_one_call_backward(monkeypatch):
+    """The autograd function bins on a side stream during the forward; the
+    result equals the one-call backward (MUSPACE_EARLY_BINNING=0), and a
+    second backward (retain_graph) takes the one-call path."""
+    def grads(early):
+        monkeypatch.setenv("MUSPACE_EARLY_BINNING", "1" if early else "0")
+        value, shapes, starts, loc, attn = _fixture(device=DEV, batch=2, queries=300, heads=8,
+                                                    embed_dims=32, levels=((20, 30), (10, 15)),
+                                                    points=4)
+        out = multi_scale_deformable_attn(value, shapes, starts, loc, attn)
+        g = torch.randn(out.shape, generator=torch.Generator().manual_seed(3)).to(DEV)
+        (out * g).sum().backward(retain_graph=True)
+        first = [t.grad.clone() for t in (value, loc, attn)]
+        for t in (value, loc, attn):
+            t.grad = None
+        (out * g).sum().backward()
+        second = [t.grad.clone() for t in (value, loc, attn)]
+        return first, second
+
+    early_first, early_second = grads(True)
+    late_first, _ = grads(False)
+    for a, b, c in zip(early_first, early_second, late_first):
+        torch.testing.assert_close(a, c, rtol=1e-6, atol=1e-6)
+        torch.testing.assert_close(b, c, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("embed_dims", [32, 3])
+def test_split_backward_entry_points_match_the_one_call(embed_dims):
+    """ms_deform_attn_backward_bin on a second stream, then _rest on the main
+    stream, against ms_deform_attn_backward_ws (C = 3 takes the atomic path:
+    nothing to bin, all of it in _rest)."""
+    from muspace_amd.runtime.native import load_native_module
+
+    lib = load_native_module()
+    value, shapes, starts, loc, attn = _fixture(device=DEV, batch=2, queries=200, heads=4,
+                                                embed_dims=embed_dims, levels=((16, 24), (8, 12)),
+                                                points=4, requires_grad=False)
+    grad = torch.randn((2, 200, 4 * embed_dims), generator=torch.Generator().manual_seed(4))
+    grad = grad.to(DEV)
+
+    def buffers():
+        return (torch.empty(value.shape, device=DEV), torch.empty(loc.shape, device=DEV),
+                torch.empty(attn.shape, device=DEV))
+
+    ref = buffers()
+    lib.ms_deform_attn_backward(value, shapes, starts, loc, attn, grad, *ref, 64)
+    got = buffers()
+    ws = lib.backward_workspace(value, loc)
+    side = torch.cuda.Stream()
+    ready = torch.cuda.Event()
+    ready.record(torch.cuda.current_stream())
+    side.wait_event(ready)
+    lib.ms_deform_attn_backward_bin(value, shapes, starts, loc, attn, *got, 64, ws, stream=side)
+    done = torch.cuda.Event()
+    done.record(side)
+    torch.cuda.current_stream().wait_event(done)
+    lib.ms_deform_attn_backward_rest(value, shapes, starts, loc, attn, grad, *got, 64, ws)
+    for a, b in zip(got, ref):
+        torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-6)
