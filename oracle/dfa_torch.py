@@ -13,7 +13,9 @@ multi-scale feature aggregation) as the reference defines it:
 * ``aggregate_batched`` computes the same sum with one index_select per
   (camera, scale, corner) over every (batch, anchor, point), written
   independently of the loop form, for shapes the loop cannot reach. It runs on
-  whatever device its inputs live on.
+  whatever device its inputs live on. Skipped points (NaN included) get a
+  finite stand-in location before any arithmetic, so their zero mask is exact
+  in the output and in every gradient, as the loop form's `continue` is.
 
 Both are differentiable; the backward oracle is autograd of either.
 """
@@ -77,6 +79,10 @@ def aggregate_batched(mc_ms_feat, spatial_shape, scale_start_index, sampling_loc
         x = sampling_location[:, :, :, c, 0]
         y = sampling_location[:, :, :, c, 1]
         inside = (x > 0) & (x < 1) & (y > 0) & (y < 1)
+        # skipped points (NaN included) take a finite stand-in, so that no NaN
+        # reaches a product with a zero mask in the output or the gradients
+        x = torch.where(inside, x, torch.full_like(x, 0.5))
+        y = torch.where(inside, y, torch.full_like(y, 0.5))
         for s in range(scales):
             height, width = (int(v) for v in spatial_shape[c, s].tolist())
             start = int(scale_start_index[c, s])

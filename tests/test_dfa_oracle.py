@@ -81,6 +81,27 @@ def test_oracle_forms_agree(seed):
     assert loops.abs().sum() > 0
 
 
+def test_oracle_forms_agree_on_nan_locations_and_gradients():
+    """A NaN location is skipped by both forms, in the output and in every gradient
+    (reference kernel: deformable_aggregation_musa.mu:376, the open-interval test is false
+    for NaN)."""
+    case = [t.requires_grad_(t.is_floating_point()) for t in random_case(7)]
+    with torch.no_grad():
+        case[3][1, 2, 0, 1, 0] = float("nan")
+        case[3][0, 1, 1, 0, 1] = float("nan")
+    twin = [t.detach().clone().requires_grad_(t.is_floating_point()) for t in case]
+    loops = dfa_torch.aggregate_loops(*case)
+    batched = dfa_torch.aggregate_batched(*twin)
+    assert torch.isfinite(batched).all()
+    torch.testing.assert_close(batched, loops, rtol=1e-12, atol=1e-12)
+    grad = torch.randn(loops.shape, generator=torch.Generator().manual_seed(1), dtype=loops.dtype)
+    (loops * grad).sum().backward()
+    (batched * grad).sum().backward()
+    for i in (0, 3, 4):
+        assert torch.isfinite(twin[i].grad).all()
+        torch.testing.assert_close(twin[i].grad, case[i].grad, rtol=1e-12, atol=1e-12)
+
+
 def test_oracle_constant_field():
     """Feature 3 everywhere and every corner inside its map: each active
     (point, camera, scale) adds 3 * its group weight."""

@@ -155,3 +155,104 @@ def test_sparsedrive_patched_entry_runs_the_hip_kernels(monkeypatch):
         torch.testing.assert_close(out.cpu(), SMALL_EXPECTED, rtol=1e-5, atol=1e-5)
     finally:
         patcher.restore()
+
+
+# --- backward contract at medium shapes ------------------------------------------------------
+
+def _oracle_grads(case, grad_out):
+    """Expected (grad_mc_ms_feat, grad_sampling_location, grad_weights) in float64 on the CPU."""
+    ref = _reference_copy(case)
+    out = dfa_torch.aggregate_batched(*ref)
+    (out * grad_out.cpu().double()).sum().backward()
+    return ref[0].grad, ref[3].grad, ref[4].grad
+
+
+def _backward_opt(case, grad_out, init_feat=None, init_other=None):
+    """deformable_aggregation_backward_opt through the C-ABI on buffers that start at
+    init_feat (grad_mc_ms_feat) and init_other (the location and weight gradients)."""
+    lib = load_native_module()
+    mc, spatial, start, loc, weights = _to_device(case, requires_grad=False)
+    gf = torch.zeros_like(mc) if init_feat is None else init_feat.clone()
+    gl = torch.zeros_like(loc) if init_other is None else torch.full_like(loc, init_other)
+    gw = torch.zeros_like(weights) if init_other is None else torch.full_like(weights, init_other)
+    lib.deformable_aggregation_backward_opt(mc, spatial, start, loc, weights,
+                                            grad_out.to(DEV).float(), gf, gl, gw)
+    torch.cuda.synchronize()
+    return gf, gl, gw
+
+
+# Location gradients at these shapes sum about 1000 fp32 products of size up to ~W = 30 per
+# element, so fp32 rounding alone leaves ~1e-4 absolute: they are held to the reference tests'
+# gradient bar (tests/ops/test_deformable_aggregation.py:194-227, 1e-3), the feature and weight
+# gradients to 1e-4.
+LOC_TOL = dict(rtol=1e-4, atol=1e-3)
+
+
+def _medium_case(seed, channels, groups, anchors=300):
+    """Locations on a 1/4096 grid: x * W - 0.5 is then exact in float32, so the kernels'
+    cell coordinates equal the float64 oracle's. (Off the grid, one float32 ulp of a
+    coordinate near 30 moves a location gradient by about a * W^2 * |D| * 2e-6, up to
+    1e-3 here: a second-order effect of the input rounding, not of the kernels.)"""
+    case = list(random_case(seed, batch=2, anchors=anchors, pts=5, cams=3,
+                            shapes=((20, 30), (10, 15), (5, 8), (3, 4)), channels=channels,
+                            groups=groups))
+    loc = case[3]
+    loc.copy_(torch.round(loc * 4096) / 4096)
+    loc[1, 7, 2, 1] = float("nan")  # a NaN location is skipped
+    loc[1, 8, 0, 2] = torch.tensor([1 / 4096, 1 - 1 / 4096], dtype=loc.dtype)  # edge corners
+    return case
+
+
+@pytest.mark.parametrize("channels,groups", [(128, 8), (256, 8), (256, 4), (96, 3)])
+def test_medium_backward_matches_the_oracle(channels, groups):
+    """Groups of 16, 32, 64 (row kernels) and 32 channels (generic kernel, C = 96): 300
+    anchors, 12 (camera, scale) maps of up to 20 x 30 cells; NaN and near-edge locations."""
+    case = _medium_case(5, channels, groups)
+    grad_out = torch.randn(2, 300, channels, generator=torch.Generator().manual_seed(6))
+    gf, gl, gw = _backward_opt(case, grad_out)
+    ef, el, ew = _oracle_grads(case, grad_out)
+    torch.testing.assert_close(gf.cpu().double(), ef, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(gl.cpu().double(), el, **LOC_TOL)
+    torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("channels,groups", [(256, 8), (64, 8)])
+def test_backward_adds_into_grad_feat_and_writes_the_others(channels, groups):
+    """The reference's contract (deformable_aggregation_musa.mu:411-428): grad_mc_ms_feat
+    is added into, the location and weight gradients are stored (groups of 32 and of 8)."""
+    case = _medium_case(8, channels, groups, anchors=40)
+    grad_out = torch.randn(2, 40, channels, generator=torch.Generator().manual_seed(9))
+    init = torch.randn(case[0].shape, generator=torch.Generator().manual_seed(10))
+    gf, gl, gw = _backward_opt(case, grad_out, init_feat=init.to(DEV).float(), init_other=7.0)
+    ef, el, ew = _oracle_grads(case, grad_out)
+    torch.testing.assert_close(gf.cpu().double(), ef + init.double(), rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(gl.cpu().double(), el, **LOC_TOL)
+    torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4)
+
+
+def test_overlapping_maps_add_both_contributions():
+    """Maps that share cells (start indexes are inputs: the reference's nested
+    feature_maps_format, mu_space/ops/deformable_aggregation.py:399-404, restarts them at 0
+    per group): both maps' contributions reach the shared rows."""
+    case = _medium_case(11, 256, 8, anchors=60)
+    spatial, start = case[1], case[2]
+    spatial[1] = spatial[0]
+    start[1] = start[0]  # camera 1 reads camera 0's maps
+    grad_out = torch.randn(2, 60, 256, generator=torch.Generator().manual_seed(12))
+    gf, gl, gw = _backward_opt(case, grad_out)
+    ef, el, ew = _oracle_grads(case, grad_out)
+    torch.testing.assert_close(gf.cpu().double(), ef, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(gl.cpu().double(), el, **LOC_TOL)
+    torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4)
+
+
+def test_backward_twice_with_a_smaller_case():
+    """Two calls in a row, the second smaller: nothing of the first call leaks into it."""
+    for anchors in (300, 37):
+        case = _medium_case(13, 256, 8, anchors=anchors)
+        grad_out = torch.randn(2, anchors, 256, generator=torch.Generator().manual_seed(14))
+        gf, gl, gw = _backward_opt(case, grad_out)
+        ef, el, ew = _oracle_grads(case, grad_out)
+        torch.testing.assert_close(gf.cpu().double(), ef, rtol=1e-4, atol=1e-4)
+        torch.testing.assert_close(gl.cpu().double(), el, **LOC_TOL)
+        torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4)
