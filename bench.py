@@ -279,6 +279,65 @@ def time_sca(lib, steps: int = 50, warmup: int = 10) -> dict:
     return res
 
 
+def time_softmax(lib, steps: int = 50, warmup: int = 10) -> dict:
+    """The attention softmax fused into MSDA at c2 (logits in, softmax over
+    each query's L*P samples per head) against torch.softmax followed by the
+    operator: the kernels alone (native calls, no autograd), the forward
+    through the operators, and forward + backward steps."""
+    from muspace_amd.ops import (attention_softmax, multi_scale_deformable_attn,
+                                 multi_scale_deformable_attn_softmax)
+
+    cfg = CONFIGS["c2"]
+    t = make_inputs(cfg, value_dtype=torch.float32, device="cuda")
+    value, shapes, starts, loc = (t["value"], t["spatial_shapes"], t["level_start_index"],
+                                  t["sampling_locations"])
+    g = torch.Generator(device="cpu").manual_seed(5)
+    logits = torch.randn(t["attention_weights"].shape, generator=g).to("cuda")
+    out = torch.empty((cfg.batch, cfg.queries, cfg.heads * cfg.channels), device="cuda")
+    grad = t["grad_output"]
+
+    def fused_kernel():
+        lib.ms_deform_attn_forward_softmax(value, shapes, starts, loc, logits, out, 64)
+
+    def unfused_kernels():
+        lib.ms_deform_attn_forward(value, shapes, starts, loc, attention_softmax(logits), out, 64)
+
+    def fwd(fused):
+        def run():
+            with torch.no_grad():
+                if fused:
+                    multi_scale_deformable_attn_softmax(value, shapes, starts, loc, logits)
+                else:
+                    multi_scale_deformable_attn(value, shapes, starts, loc,
+                                                attention_softmax(logits))
+        return run
+
+    leaves = [x.detach().requires_grad_(True) for x in (value, loc, logits)]
+
+    def train(fused):
+        def step():
+            v, lc, lg = leaves
+            for x in leaves:
+                x.grad = None
+            if fused:
+                y = multi_scale_deformable_attn_softmax(v, shapes, starts, lc, lg)
+            else:
+                y = multi_scale_deformable_attn(v, shapes, starts, lc, attention_softmax(lg))
+            y.backward(grad)
+        return step
+
+    return {
+        "workload": "c2 (BEVFormer SCA, bs*cams 6, 10000 queries, 8 heads x 32, 4 levels x 8 "
+                    "points), logits ~ N(0, 1)",
+        "fused_kernel_us": round(_event_ms(fused_kernel, steps, warmup) * 1e3, 1),
+        "softmax_then_kernel_us": round(_event_ms(unfused_kernels, steps, warmup) * 1e3, 1),
+        "fused_fwd_us": round(_event_ms(fwd(True), steps, warmup) * 1e3, 1),
+        "unfused_fwd_us": round(_event_ms(fwd(False), steps, warmup) * 1e3, 1),
+        "fused_fwd_bwd_us": round(_event_ms(train(True), steps // 2, warmup) * 1e3, 1),
+        "unfused_fwd_bwd_us": round(_event_ms(train(False), steps // 2, warmup) * 1e3, 1),
+    }
+
+
 def time_dfa(lib, steps: int = 50, warmup: int = 10) -> dict:
     """Deformable aggregation at SparseDrive's production shape, kernel-only
     scope as the reference's benchmark
@@ -367,6 +426,8 @@ def main() -> int:
                         help="only the fused spatial cross-attention scatter-average leg")
     parser.add_argument("--dfa-only", action="store_true",
                         help="only the deformable aggregation leg")
+    parser.add_argument("--softmax-only", action="store_true",
+                        help="only the fused attention-softmax leg (c2)")
     parser.add_argument("--serial-backward", action="store_true",
                         help="bin on the main stream (no overlap with the forward), so that "
                              "rocprofv3 sees each kernel alone")
@@ -402,6 +463,10 @@ def main() -> int:
         return 0
     if args.dfa_only:
         print(json.dumps({"sparsedrive-dfa-float32": time_dfa(lib, args.steps, args.warmup)}))
+        return 0
+    if args.softmax_only:
+        print(json.dumps({"c2-softmax-fused-float32": time_softmax(lib, args.steps,
+                                                                     args.warmup)}))
         return 0
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
@@ -440,6 +505,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         print("[bench] extra sparsedrive-dfa", file=sys.stderr, flush=True)
         extra["sparsedrive-dfa-float32"] = time_dfa(lib)
+        torch.cuda.empty_cache()
+        print("[bench] extra c2-softmax-fused", file=sys.stderr, flush=True)
+        extra["c2-softmax-fused-float32"] = time_softmax(lib)
         torch.cuda.empty_cache()
 
     cpu = None

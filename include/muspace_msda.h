@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define MUSPACE_MSDA_ABI_VERSION 2
+#define MUSPACE_MSDA_ABI_VERSION 3
 
 /* the library is built with -fvisibility=hidden; only these symbols export */
 #if defined(__GNUC__)
@@ -75,6 +75,7 @@ extern "C" {
 #define MUSPACE_EINVAL 1  /* bad argument: null pointer, negative size, dtype, im2col_step */
 #define MUSPACE_ERANGE 2  /* shape too large for the kernels' 32-bit intra-batch indexing */
 #define MUSPACE_ELAUNCH 3 /* the HIP runtime rejected a launch */
+#define MUSPACE_ENOMEM 4  /* stream-ordered scratch could not be allocated */
 
 /* Forward: output = MSDA(value, geometry). Replaces ms_deform_attn_forward
  * (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:507-560). */
@@ -213,6 +214,65 @@ MUSPACE_API int ms_deform_attn_scatter_div_grad(const void *grad_slots, int valu
                                                 void *grad_output, int64_t batch,
                                                 int64_t num_cams, int64_t max_len,
                                                 int64_t num_query, int64_t row, void *stream);
+
+/* Softmax over L*P fused into the operator (producer side of the path:
+ * BEVFormer's MSDeformableAttention3D and friends apply
+ *   attention_weights = logits.view(bs, nq, M, L*P).softmax(-1)
+ * before calling the reference's ms_deform_attn_forward; no reference
+ * counterpart). `attention_logits` has the shape and dtype of
+ * attention_weights; each (b, q, m) unit's L*P weights are the softmax of its
+ * logits (an all -inf unit gives NaN, as torch.softmax does). Otherwise the
+ * contract of ms_deform_attn_forward. The row kernels fuse the softmax into
+ * their prologue; other shapes run a standalone softmax into stream-ordered
+ * scratch (MUSPACE_ENOMEM if it cannot be allocated). */
+MUSPACE_API int ms_deform_attn_forward_softmax(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_logits, int geometry_dtype, void *output, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *stream);
+
+/* Scratch bytes of the softmax backward (the probabilities, then the
+ * binning scratch of ms_deform_attn_backward_workspace_size when the tile path
+ * applies); 0 when nothing is sampled or the dims are invalid. */
+MUSPACE_API size_t ms_deform_attn_backward_softmax_workspace_size(
+    int value_dtype, int geometry_dtype, int64_t batch, int64_t spatial_size, int64_t num_heads,
+    int64_t channels, int64_t num_levels, int64_t num_query, int64_t num_point);
+
+/* Backward of ms_deform_attn_forward_softmax in two calls on one workspace
+ * (256-byte aligned, at least the size above; MUSPACE_EINVAL otherwise), as
+ * ms_deform_attn_backward_bin / _rest: _bin reads the geometry and logits only
+ * (grad_output may be NULL) and writes the probabilities and the binning into
+ * the workspace; _rest writes grad_value, grad_sampling_locations and
+ * grad_attention_logits = p * (g - sum_j p_j g_j) per unit, g being the
+ * gradient of the softmax weights. */
+MUSPACE_API int ms_deform_attn_backward_softmax_bin(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_logits, int geometry_dtype, const void *grad_output, float *grad_value,
+    float *grad_sampling_locations, float *grad_attention_logits, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+MUSPACE_API int ms_deform_attn_backward_softmax_rest(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_logits, int geometry_dtype, const void *grad_output, float *grad_value,
+    float *grad_sampling_locations, float *grad_attention_logits, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+/* Both parts in one call with stream-ordered scratch (MUSPACE_ENOMEM if it
+ * cannot be allocated). */
+MUSPACE_API int ms_deform_attn_backward_softmax(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_logits, int geometry_dtype, const void *grad_output, float *grad_value,
+    float *grad_sampling_locations, float *grad_attention_logits, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *stream);
 
 /* Build smoke: y[i] = x[i] + 1 for i < n (float32). Mirrors add_one
  * (/root/reference/csrc/ffi/muspace_ops.mu:40-55). */

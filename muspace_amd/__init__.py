@@ -12,6 +12,7 @@ from .ops import (
     multi_scale_deformable_attn_pytorch,
     multi_scale_deformable_attn_pytorch_compat,
     multi_scale_deformable_attn_scatter_div,
+    multi_scale_deformable_attn_softmax,
 )
 from .runtime.kernel_dispatch import (
     DispatchDecision,
@@ -35,4 +36,5 @@ __all__ = [
     "multi_scale_deformable_attn_pytorch",
     "multi_scale_deformable_attn_pytorch_compat",
     "multi_scale_deformable_attn_scatter_div",
+    "multi_scale_deformable_attn_softmax",
 ]

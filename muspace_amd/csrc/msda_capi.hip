@@ -235,6 +235,102 @@ void launch_forward(const void *value, const int64_t *shapes, const int64_t *sta
   }
 }
 
+// ------------------------------------------------- softmax over L*P (fused) ---
+
+// The standalone softmax kernels: four samples per lane in registers when
+// L*P is a multiple of 4 up to 64 (rows of 16 or 8 bytes per lane), else a
+// strided loop. Lanes per unit: pow2 >= L*P / 4, at most 16.
+bool softmax_by_four(const msda::Shape &s) { return s.lp % 4 == 0 && s.lp <= 64; }
+
+int softmax_lanes_log2(const msda::Shape &s) {
+  int w = pow2_ceil(s.lp > 0 ? (s.lp + 3) / 4 : 1);
+  if (w > 16) w = 16;
+  return log2_int(w);
+}
+
+int softmax_blocks(const msda::Shape &s) {
+  const int64_t lanes = static_cast<int64_t>(s.units) << softmax_lanes_log2(s);
+  return static_cast<int>((lanes + msda::kBlock - 1) / msda::kBlock);
+}
+
+template <typename GT>
+void launch_softmax(const void *logits, void *probs, const msda::Shape &s, hipStream_t st) {
+  const GT *x = static_cast<const GT *>(logits);
+  GT *p = static_cast<GT *>(probs);
+  if (softmax_by_four(s) && aligned(logits, 4 * sizeof(GT))) {
+    msda::msda_softmax_units4<GT><<<softmax_blocks(s), msda::kBlock, 0, st>>>(
+        x, p, s, softmax_lanes_log2(s));
+  } else {
+    msda::msda_softmax_units<GT><<<softmax_blocks(s), msda::kBlock, 0, st>>>(
+        x, p, s, softmax_lanes_log2(s));
+  }
+}
+
+template <typename GT>
+void launch_softmax_backward(const void *probs, float *grad, const msda::Shape &s,
+                             hipStream_t st) {
+  const GT *p = static_cast<const GT *>(probs);
+  if (softmax_by_four(s) && aligned(grad, 16)) {
+    msda::msda_softmax_backward_units4<GT><<<softmax_blocks(s), msda::kBlock, 0, st>>>(
+        p, grad, s, softmax_lanes_log2(s));
+  } else {
+    msda::msda_softmax_backward_units<GT><<<softmax_blocks(s), msda::kBlock, 0, st>>>(
+        p, grad, s, softmax_lanes_log2(s));
+  }
+}
+
+size_t probs_bytes(const msda::Shape &s, int geometry_dtype) {
+  const size_t gb = geometry_dtype == MUSPACE_DTYPE_F32 ? 4 : 2;
+  return (static_cast<size_t>(s.units) * s.lp * gb + 255) & ~static_cast<size_t>(255);
+}
+
+template <typename VT, typename GT, int C>
+void launch_forward_softmax_rows(const void *value, const int64_t *shapes, const int64_t *starts,
+                                 const void *loc, const void *logits, void *out,
+                                 const msda::Shape &s, hipStream_t st) {
+  const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
+  forward_rows_ns<VT, C>(s, [&](auto ns, const Launch &L) {
+    msda::msda_forward_softmax_rows<VT, GT, C, decltype(ns)::value>
+        <<<L.blocks, msda::kBlock, 0, st>>>(static_cast<const VT *>(value), vbytes, shapes,
+                                            starts, static_cast<const GT *>(loc),
+                                            static_cast<const GT *>(logits),
+                                            static_cast<VT *>(out), s, L.plan);
+  });
+}
+
+// Forward with logits: the row kernels fuse the softmax; other shapes take the
+// standalone softmax into stream-ordered scratch, then the generic kernel.
+// Returns false when that scratch cannot be allocated.
+template <typename VT, typename GT>
+bool launch_forward_softmax(const void *value, const int64_t *shapes, const int64_t *starts,
+                            const void *loc, const void *logits, void *out,
+                            const msda::Shape &s, int geometry_dtype, hipStream_t st) {
+  const bool small = value_bytes(s, sizeof(VT)) + 64 <= msda::kOobOffset;
+  const int rows = rows_aligned({value, out}) && small ? s.channels : 0;
+  switch (rows) {
+    case 16:
+      launch_forward_softmax_rows<VT, GT, 16>(value, shapes, starts, loc, logits, out, s, st);
+      return true;
+    case 32:
+      launch_forward_softmax_rows<VT, GT, 32>(value, shapes, starts, loc, logits, out, s, st);
+      return true;
+    case 64:
+      launch_forward_softmax_rows<VT, GT, 64>(value, shapes, starts, loc, logits, out, s, st);
+      return true;
+    default: {
+      void *probs = nullptr;
+      if (hipMallocAsync(&probs, probs_bytes(s, geometry_dtype), st) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+      }
+      launch_softmax<GT>(logits, probs, s, st);
+      launch_forward<VT, GT>(value, shapes, starts, loc, probs, out, s, st);
+      (void)hipFreeAsync(probs, st);
+      return true;
+    }
+  }
+}
+
 // ------------------------------------------ spatial cross-attention epilogue ---
 
 // Camera-rebatched dims of the scatter-average entry points.
@@ -676,7 +772,7 @@ int backward_impl(const char *fn, const void *value, int value_dtype,
                   int geometry_dtype, const void *grad_output, float *grad_value,
                   float *grad_sampling_locations, float *grad_attention_weights, const Args &a,
                   void *workspace, size_t workspace_bytes, hipStream_t st,
-                  Phase phase = Phase::kAll) {
+                  Phase phase = Phase::kAll, bool softmax = false) {
   msda::Shape s;
   if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
   const int64_t nvalue = a.batch * a.spatial * a.heads * a.channels;
@@ -695,13 +791,43 @@ int backward_impl(const char *fn, const void *value, int value_dtype,
       !grad_attention_weights) {
     return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
   }
+  if (!softmax) {
+    with_dtypes(value_dtype, geometry_dtype, [&](auto vt, auto gt) {
+      launch_backward<decltype(vt), decltype(gt)>(
+          value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+          grad_output, grad_value, grad_sampling_locations, grad_attention_weights, s, workspace,
+          workspace_bytes, phase, st);
+    });
+    return check_launch(fn);
+  }
+  // attention_weights are logits: the binning part writes their softmax to the
+  // head of the workspace and bins with it; the rest turns the weight gradient
+  // into the logit gradient in place
+  const size_t pb = probs_bytes(s, geometry_dtype);
+  if (!workspace || workspace_bytes < pb || !aligned(workspace, 256)) {
+    return fail(MUSPACE_EINVAL, "%s: workspace of %zu bytes (256-byte aligned) required, got %zu",
+                fn, pb, workspace_bytes);
+  }
+  void *probs = workspace;
+  void *tiles = static_cast<unsigned char *>(workspace) + pb;
   with_dtypes(value_dtype, geometry_dtype, [&](auto vt, auto gt) {
-    launch_backward<decltype(vt), decltype(gt)>(
-        value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
-        grad_output, grad_value, grad_sampling_locations, grad_attention_weights, s, workspace,
-        workspace_bytes, phase, st);
+    using VT = decltype(vt);
+    using GT = decltype(gt);
+    if (phase != Phase::kRest) launch_softmax<GT>(attention_weights, probs, s, st);
+    launch_backward<VT, GT>(value, spatial_shapes, level_start_index, sampling_locations, probs,
+                            grad_output, grad_value, grad_sampling_locations,
+                            grad_attention_weights, s, tiles, workspace_bytes - pb, phase, st);
+    if (phase != Phase::kBin) launch_softmax_backward<GT>(probs, grad_attention_weights, s, st);
   });
   return check_launch(fn);
+}
+
+// Scratch of the softmax backward: the probabilities, then the tile path's
+// workspace when it applies.
+size_t softmax_workspace_bytes(const msda::Shape &s, int value_dtype, int geometry_dtype) {
+  TileWorkspace w;
+  const size_t tiles = plan_tile_workspace(s, value_dtype, w) ? w.bytes : 0;
+  return probs_bytes(s, geometry_dtype) + tiles;
 }
 
 }  // namespace
@@ -1011,6 +1137,116 @@ int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *s
                                sampling_locations, attention_weights, geometry_dtype, grad_output,
                                grad_value, grad_sampling_locations, grad_attention_weights, a,
                                workspace, bytes, st);
+  if (workspace) (void)hipFreeAsync(workspace, st);
+  return rc;
+}
+
+int ms_deform_attn_forward_softmax(const void *value, int value_dtype,
+                                   const int64_t *spatial_shapes,
+                                   const int64_t *level_start_index,
+                                   const void *sampling_locations, const void *attention_logits,
+                                   int geometry_dtype, void *output, int64_t batch,
+                                   int64_t spatial_size, int64_t num_heads, int64_t channels,
+                                   int64_t num_levels, int64_t num_query, int64_t num_point,
+                                   int64_t im2col_step, void *stream) {
+  static const char *fn = "ms_deform_attn_forward_softmax";
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  msda::Shape s;
+  if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
+  if (!needs_data(s)) return ok();
+  if (!output || ((!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+                   !attention_logits) &&
+                  s.lp > 0)) {
+    return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  bool launched = true;
+  with_dtypes(value_dtype, geometry_dtype, [&](auto vt, auto gt) {
+    launched = launch_forward_softmax<decltype(vt), decltype(gt)>(
+        value, spatial_shapes, level_start_index, sampling_locations, attention_logits, output, s,
+        geometry_dtype, st);
+  });
+  if (!launched) return fail(MUSPACE_ENOMEM, "%s: scratch allocation failed", fn);
+  return check_launch(fn);
+}
+
+size_t ms_deform_attn_backward_softmax_workspace_size(int value_dtype, int geometry_dtype,
+                                                      int64_t batch, int64_t spatial_size,
+                                                      int64_t num_heads, int64_t channels,
+                                                      int64_t num_levels, int64_t num_query,
+                                                      int64_t num_point) {
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               batch > 0 ? batch : 1};
+  msda::Shape s;
+  if (validate("ms_deform_attn_backward_softmax_workspace_size", a, value_dtype, geometry_dtype,
+               s)) {
+    return 0;
+  }
+  ok();
+  if (!needs_data(s) || s.lp == 0) return 0;
+  return softmax_workspace_bytes(s, value_dtype, geometry_dtype);
+}
+
+int ms_deform_attn_backward_softmax_bin(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_logits, int geometry_dtype, const void *grad_output, float *grad_value,
+    float *grad_sampling_locations, float *grad_attention_logits, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  return backward_impl("ms_deform_attn_backward_softmax_bin", value, value_dtype, spatial_shapes,
+                       level_start_index, sampling_locations, attention_logits, geometry_dtype,
+                       grad_output, grad_value, grad_sampling_locations, grad_attention_logits,
+                       a, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                       Phase::kBin, true);
+}
+
+int ms_deform_attn_backward_softmax_rest(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_logits, int geometry_dtype, const void *grad_output, float *grad_value,
+    float *grad_sampling_locations, float *grad_attention_logits, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  return backward_impl("ms_deform_attn_backward_softmax_rest", value, value_dtype, spatial_shapes,
+                       level_start_index, sampling_locations, attention_logits, geometry_dtype,
+                       grad_output, grad_value, grad_sampling_locations, grad_attention_logits,
+                       a, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
+                       Phase::kRest, true);
+}
+
+int ms_deform_attn_backward_softmax(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_logits, int geometry_dtype, const void *grad_output, float *grad_value,
+    float *grad_sampling_locations, float *grad_attention_logits, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *stream) {
+  static const char *fn = "ms_deform_attn_backward_softmax";
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  msda::Shape s;
+  if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
+  // stream-ordered scratch (probabilities and binning); freed in stream order
+  const size_t bytes =
+      needs_data(s) && s.lp > 0 ? softmax_workspace_bytes(s, value_dtype, geometry_dtype) : 0;
+  void *workspace = nullptr;
+  if (bytes > 0 && hipMallocAsync(&workspace, bytes, st) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(MUSPACE_ENOMEM, "%s: scratch allocation of %zu bytes failed", fn, bytes);
+  }
+  const int rc = backward_impl(fn, value, value_dtype, spatial_shapes, level_start_index,
+                               sampling_locations, attention_logits, geometry_dtype, grad_output,
+                               grad_value, grad_sampling_locations, grad_attention_logits, a,
+                               workspace, bytes, st, Phase::kAll, true);
   if (workspace) (void)hipFreeAsync(workspace, st);
   return rc;
 }

@@ -221,6 +221,75 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// The same with the group width n (a power of two <= 64) known at run time;
+// n must be uniform across the wavefront. Groups of 32 and 64 combine the
+// four 16-lane row totals through readlane (VALU) instead of an LDS-routed
+// shuffle.
+template <typename Op>
+__device__ __forceinline__ float combine_rows(float v, int n, Op op) {
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  const float lo = op(r0, r1), hi = op(r2, r3);
+  if (n == 64) return op(lo, hi);
+  return (threadIdx.x % kWave) < 32 ? lo : hi;
+}
+
+// Branch-free forms for a run-time width n >= 1 (uniform): every DPP step is
+// computed and a uniform select keeps it only where n asks for it, so the
+// reduction is straight-line code the scheduler can interleave with other work.
+template <typename Op>
+__device__ __forceinline__ float group_reduce_sel(float v, int n, Op op) {
+  float w = op(v, MSDA_DPP(v, 0xB1));
+  v = n >= 2 ? w : v;
+  w = op(v, MSDA_DPP(v, 0x4E));
+  v = n >= 4 ? w : v;
+  w = op(v, MSDA_DPP(v, 0x141));
+  v = n >= 8 ? w : v;
+  w = op(v, MSDA_DPP(v, 0x140));
+  v = n >= 16 ? w : v;
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  const float lo = op(r0, r1), hi = op(r2, r3);
+  const float wide = n >= 64 ? op(lo, hi) : ((threadIdx.x % kWave) < 32 ? lo : hi);
+  return n >= 32 ? wide : v;
+}
+
+__device__ __forceinline__ float group_sum_sel(float v, int n) {
+  return group_reduce_sel(v, n, [](float x, float y) { return x + y; });
+}
+
+__device__ __forceinline__ float group_max_sel(float v, int n) {
+  return group_reduce_sel(v, n, [](float x, float y) { return fmaxf(x, y); });
+}
+
+__device__ __forceinline__ float group_sum_n(float v, int n) {
+  switch (n) {
+    case 1: return v;
+    case 2: return group_sum<2>(v);
+    case 4: return group_sum<4>(v);
+    case 8: return group_sum<8>(v);
+    case 16: return group_sum<16>(v);
+    default:
+      return combine_rows(group_sum<16>(v), n, [](float x, float y) { return x + y; });
+  }
+}
+
+__device__ __forceinline__ float group_max_n(float v, int n) {
+  switch (n) {
+    case 1: return v;
+    case 2: return group_max<2>(v);
+    case 4: return group_max<4>(v);
+    case 8: return group_max<8>(v);
+    case 16: return group_max<16>(v);
+    default:
+      return combine_rows(group_max<16>(v), n, [](float x, float y) { return fmaxf(x, y); });
+  }
+}
+
 // ------------------------------------------------------- buffer loads ---
 
 // Raw buffer loads over a tensor of `bytes` bytes: a 16-byte load at an

@@ -243,7 +243,17 @@ struct CameraSlots {
 // in issue order), and every load is unconditional (clamped indices): a load
 // inside a branch is waited for before the branch joins.
 // value_bytes < 2^31 (checked on the host) keeps every offset in 32 bits.
-template <typename VT, typename GT, int C, int NS, typename Out>
+//
+// kSoftmax: `attn` holds logits, and each unit's weights are their softmax
+// over its L*P samples. A unit's tap lanes are one aligned block of GU*NS
+// lanes, so the softmax is a running max and sum over that block (DPP and
+// readlane reductions) per step, the online form: a step that raises the
+// unit's max rescales the accumulators by exp(old max - new max), and the
+// unit's row is scaled by 1/sum before it is stored. When a unit fits one
+// step (the common case, L*P <= GU*NS) that is the plain exp(x - max) / sum.
+// The reductions are branch-free (every step computed, uniform selects), so
+// they schedule with the tap's own arithmetic.
+template <typename VT, typename GT, int C, int NS, typename Out, bool kSoftmax = false>
 __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint32_t value_bytes,
                                              const int64_t *__restrict__ shapes,
                                              const int64_t *__restrict__ starts,
@@ -260,6 +270,8 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   __shared__ Level lv[kMaxLevels];
   __shared__ u32x4 tap_off[kBlock];
   __shared__ float4 tap_w[kBlock];
+  // kSoftmax, per unit slot: the current step's rescale and 1/sum
+  __shared__ float2 unit_norm[kSoftmax ? kBlock : 1];
   stage_levels(lv, shapes, starts, s);
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(value, value_bytes);
 
@@ -298,6 +310,29 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   bool ok;
   int sm;
   uint32_t unit_base;  // byte offset of the tap unit's (b, head m) in value
+  // kSoftmax: the tap unit's running max and sum, and this lane's weight
+  // exp(x - max) for the current step
+  float m_run = 0.0f, s_run = 0.0f, e_cur = 0.0f;
+  auto softmax_step = [&](int st) {  // the logit of step st is `a`
+    const int tb = GU * NS;  // the unit's tap lanes: an aligned block
+    const float x = ok ? a : -INFINITY;
+    const float mx = group_max_sel(x, tb);
+    if (st % chunks == 0) {
+      m_run = -INFINITY;
+      s_run = 0.0f;
+    }
+    const float m_new = fmaxf(m_run, mx);
+    const bool none = m_new == -INFINITY;  // no finite logit yet
+    const float sc = none ? 1.0f : __expf(m_run - m_new);
+    e_cur = ok && !none ? __expf(x - m_new) : 0.0f;
+    const float es = group_sum_sel(e_cur, tb);
+    s_run = s_run * sc + es;
+    m_run = m_new;
+    if (lane < NG * NS && (lane & (tb - 1)) == 0) {
+      // hardware reciprocal (1 ulp); 1/0 = inf keeps an all -inf unit NaN
+      unit_norm[wave * kWave + tslot] = make_float2(sc, __builtin_amdgcn_rcpf(s_run));
+    }
+  };
   auto load_geometry = [&](int st) {
     const int it = st / chunks, s0 = (st % chunks) * GU * NS;
     if (st > 0 && st % chunks == 0) tu.advance(UW, s);
@@ -326,7 +361,11 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
     {
       const Level L = lv[level_of_sample(sm, s)];
       const Tap t = make_tap(lx, ly, L, ok);
-      const float ai = ok ? a : 0.0f;
+      float ai = ok ? a : 0.0f;
+      if constexpr (kSoftmax) {
+        softmax_step(st);
+        ai = e_cur;  // 0 unless ok
+      }
       const uint32_t row = static_cast<uint32_t>(MC * VB);
       const uint32_t c00 = unit_base + static_cast<uint32_t>(L.start + t.cell00) * row;
       const uint32_t c10 = c00 + static_cast<uint32_t>(L.w) * row;
@@ -352,6 +391,13 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
     }
     load_geometry(st + 1);
     // C. accumulate
+    if constexpr (kSoftmax) {
+      if (chunks > 1) {
+        const float sc = unit_norm[wave * kWave + slot].x;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) acc[j] *= sc;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const float4 w = my_w[grp * NS + j];
@@ -370,6 +416,11 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
       for (int off = KQ; off < KQ * GU; off <<= 1) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) acc[j] += __shfl_xor(acc[j], off, kWave);
+      }
+      if constexpr (kSoftmax) {
+        const float inv = unit_norm[wave * kWave + slot].y;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) acc[j] *= inv;
       }
       const int64_t u64 = u_first + static_cast<int64_t>(st / chunks) * UW + slot;
       if (u64 < s.units && gi == 0) {
@@ -397,6 +448,20 @@ __global__ void __launch_bounds__(kBlock)
                       VT *__restrict__ out, Shape s, RowPlan plan) {
   forward_rows<VT, GT, C, NS>(value, value_bytes, shapes, starts, loc, attn, DenseRows<VT>{out},
                               s, plan, xcd_logical_block(blockIdx.x, gridDim.x));
+}
+
+// Forward with the attention weights given as logits: softmax over each
+// unit's L*P samples fused into the prologue (forward_rows, kSoftmax).
+template <typename VT, typename GT, int C, int NS>
+__global__ void __launch_bounds__(kBlock)
+    msda_forward_softmax_rows(const VT *__restrict__ value, uint32_t value_bytes,
+                              const int64_t *__restrict__ shapes,
+                              const int64_t *__restrict__ starts, const GT *__restrict__ loc,
+                              const GT *__restrict__ logits, VT *__restrict__ out, Shape s,
+                              RowPlan plan) {
+  forward_rows<VT, GT, C, NS, DenseRows<VT>, true>(value, value_bytes, shapes, starts, loc,
+                                                   logits, DenseRows<VT>{out}, s, plan,
+                                                   xcd_logical_block(blockIdx.x, gridDim.x));
 }
 
 // Cameras of the spatial cross-attention, summed into the BEV slots
@@ -712,6 +777,133 @@ __global__ void __launch_bounds__(kBlock)
 
 // Fill with zeros (used before the atomic fallback backward; a kernel rather
 // than a memset so that the launch sequence is graph-capture friendly).
+// ------------------------------------------------------------ softmax ---
+
+// Softmax of each unit's L*P logits and its backward, for the paths that do
+// not fuse it (the binning of the backward, the generic and atomic kernels).
+// A unit is W <= 16 consecutive lanes (W = pow2 >= L*P / 4, so about four
+// samples per lane; the reductions stay in DPP); a lane takes the unit's
+// samples i, i + W, ... (contiguous across the unit's lanes).
+template <typename GT>
+__global__ void __launch_bounds__(kBlock)
+    msda_softmax_units(const GT *__restrict__ logits, GT *__restrict__ probs, Shape s,
+                       int w_log2) {
+  const int W = 1 << w_log2;
+  const int64_t unit =
+      (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> w_log2;
+  const int i = threadIdx.x & (W - 1);
+  const bool live = unit < s.units;
+  const GT *x = logits + (live ? unit : 0) * s.lp;
+  float mx = -INFINITY;
+  for (int j = i; j < s.lp; j += W) mx = fmaxf(mx, to_float(x[j]));
+  mx = group_max_n(mx, W);
+  const bool none = mx == -INFINITY;
+  float sum = 0.0f;
+  for (int j = i; j < s.lp; j += W) sum += none ? 0.0f : expf(to_float(x[j]) - mx);
+  sum = group_sum_n(sum, W);
+  if (!live) return;
+  const float inv = 1.0f / sum;
+  GT *p = probs + unit * s.lp;
+  for (int j = i; j < s.lp; j += W) {
+    p[j] = from_float<GT>(none ? 0.0f * inv : expf(to_float(x[j]) - mx) * inv);
+  }
+}
+
+// grad (in place) = p * (grad - sum_j p_j grad_j) over each unit's samples:
+// the weight gradient becomes the logit gradient.
+template <typename GT>
+__global__ void __launch_bounds__(kBlock)
+    msda_softmax_backward_units(const GT *__restrict__ probs, float *__restrict__ grad, Shape s,
+                                int w_log2) {
+  const int W = 1 << w_log2;
+  const int64_t unit =
+      (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> w_log2;
+  const int i = threadIdx.x & (W - 1);
+  const bool live = unit < s.units;
+  const GT *p = probs + (live ? unit : 0) * s.lp;
+  float *g = grad + (live ? unit : 0) * s.lp;
+  float dot = 0.0f;
+  for (int j = i; j < s.lp; j += W) dot += to_float(p[j]) * g[j];
+  dot = group_sum_n(dot, W);
+  if (!live) return;
+  for (int j = i; j < s.lp; j += W) g[j] = to_float(p[j]) * (g[j] - dot);
+}
+
+// Four consecutive elements as one 16-byte (fp32) or 8-byte (16-bit) access.
+__device__ __forceinline__ void load4f(const float *p, float (&v)[4]) {
+  const float4 q = *reinterpret_cast<const float4 *>(p);
+  v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+}
+template <typename T>
+__device__ __forceinline__ void load4f(const T *p, float (&v)[4]) {
+  const uint2 q = *reinterpret_cast<const uint2 *>(p);
+  const T *h = reinterpret_cast<const T *>(&q);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = to_float(h[k]);
+}
+__device__ __forceinline__ void store4f(float *p, const float (&v)[4]) {
+  *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <typename T>
+__device__ __forceinline__ void store4f(T *p, const float (&v)[4]) {
+  uint2 q;
+  T *h = reinterpret_cast<T *>(&q);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) h[k] = from_float<T>(v[k]);
+  *reinterpret_cast<uint2 *>(p) = q;
+}
+
+// The same two kernels when L*P is a multiple of 4 and at most 64: lane i of
+// a unit's W = pow2 >= L*P/4 lanes holds samples [4i, 4i + 4) in registers
+// (one access each way); lanes past L*P/4 idle.
+template <typename GT>
+__global__ void __launch_bounds__(kBlock)
+    msda_softmax_units4(const GT *__restrict__ logits, GT *__restrict__ probs, Shape s,
+                        int w_log2) {
+  const int64_t unit =
+      (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> w_log2;
+  const int i = threadIdx.x & ((1 << w_log2) - 1);
+  const bool live = unit < s.units, has = live && 4 * i < s.lp;
+  const size_t at = has ? static_cast<size_t>(unit) * s.lp + 4 * i : 0;
+  float v[4];
+  load4f(logits + at, v);
+  float mx = has ? fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])) : -INFINITY;
+  mx = group_max_n(mx, 1 << w_log2);
+  const bool none = mx == -INFINITY;
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = none ? 0.0f : expf(v[k] - mx);
+    sum += v[k];
+  }
+  sum = group_sum_n(has ? sum : 0.0f, 1 << w_log2);
+  if (!has) return;
+  const float inv = 1.0f / sum;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] *= inv;  // an all -inf unit: 0 * inf = NaN
+  store4f(probs + at, v);
+}
+
+template <typename GT>
+__global__ void __launch_bounds__(kBlock)
+    msda_softmax_backward_units4(const GT *__restrict__ probs, float *__restrict__ grad, Shape s,
+                                 int w_log2) {
+  const int64_t unit =
+      (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> w_log2;
+  const int i = threadIdx.x & ((1 << w_log2) - 1);
+  const bool live = unit < s.units, has = live && 4 * i < s.lp;
+  const size_t at = has ? static_cast<size_t>(unit) * s.lp + 4 * i : 0;
+  float p[4], g[4];
+  load4f(probs + at, p);
+  load4f(grad + at, g);
+  float dot = has ? p[0] * g[0] + p[1] * g[1] + p[2] * g[2] + p[3] * g[3] : 0.0f;
+  dot = group_sum_n(dot, 1 << w_log2);
+  if (!has) return;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) g[k] = p[k] * (g[k] - dot);
+  store4f(grad + at, g);
+}
+
 __global__ void __launch_bounds__(kBlock) zero_kernel(float *x, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {

@@ -8,6 +8,7 @@ from .multi_scale_deformable_attn import (
     multi_scale_deformable_attn_pytorch_compat,
 )
 from .scatter_div import multi_scale_deformable_attn_scatter_div
+from .msda_softmax import attention_softmax, multi_scale_deformable_attn_softmax
 from .deformable_aggregation import (
     deformable_aggregation,
     deformable_aggregation_function,
@@ -16,6 +17,7 @@ from .deformable_aggregation import (
 )
 
 __all__ = [
+    "attention_softmax",
     "deformable_aggregation",
     "deformable_aggregation_function",
     "deformable_aggregation_reference",
@@ -26,4 +28,5 @@ __all__ = [
     "multi_scale_deformable_attn_pytorch",
     "multi_scale_deformable_attn_pytorch_compat",
     "multi_scale_deformable_attn_scatter_div",
+    "multi_scale_deformable_attn_softmax",
 ]

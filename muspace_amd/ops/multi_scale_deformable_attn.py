@@ -142,6 +142,14 @@ def _early_binning_enabled() -> bool:
     return os.environ.get(EARLY_BINNING_ENV, "1").strip().lower() not in {"0", "false", "no", "off"}
 
 
+def _bins_early(*tensors: torch.Tensor) -> bool:
+    """Whether a forward should start its backward's binning: a graph will be
+    recorded (grad mode on, which Function.forward itself cannot see) and an
+    input needs a gradient."""
+    return (_early_binning_enabled() and torch.is_grad_enabled()
+            and any(t.requires_grad for t in tensors))
+
+
 def _side_stream(device: torch.device) -> torch.cuda.Stream:
     index = device.index if device.index is not None else torch.cuda.current_device()
     stream = _SIDE_STREAMS.get(index)
@@ -189,6 +197,7 @@ class _NativeMSDAFunction(torch.autograd.Function):
         sampling_locations: torch.Tensor,
         attention_weights: torch.Tensor,
         im2col_step: int,
+        early_binning: bool = False,
     ) -> torch.Tensor:
         ext = _native_extension()
         if ext is None:
@@ -207,7 +216,7 @@ class _NativeMSDAFunction(torch.autograd.Function):
             (value_arg.size(0), sampling_arg.size(1), value_arg.size(2) * value_arg.size(3))
         )
         ctx.binned = None
-        if _early_binning_enabled() and any(ctx.needs_input_grad[i] for i in (0, 3, 4)):
+        if early_binning and any(ctx.needs_input_grad[i] for i in (0, 3, 4)):
             ctx.binned = _start_binning(ext, value_arg, spatial_arg, start_arg, sampling_arg,
                                         attn_arg, im2col_step)
         ext.ms_deform_attn_forward(
@@ -261,6 +270,7 @@ class _NativeMSDAFunction(torch.autograd.Function):
             None,
             grad_sampling.to(dtype=ctx.sampling_dtype),
             grad_attention.to(dtype=ctx.attention_dtype),
+            None,
             None,
         )
 
@@ -353,6 +363,7 @@ def multi_scale_deformable_attn(
             sampling_locations,
             attention_weights,
             im2col_step,
+            _bins_early(value, sampling_locations, attention_weights),
         )
     except RuntimeError as exc:
         if backend != "auto":

@@ -25,7 +25,7 @@ from pathlib import Path
 from typing import Any, Callable
 
 LIBRARY_RELPATH = "native/libmuspace_msda.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
@@ -68,6 +68,33 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
         + [_c_int64] * 8
         + [_c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "ms_deform_attn_forward_softmax": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr],
+    ),
+    "ms_deform_attn_backward_softmax_workspace_size": (
+        ctypes.c_size_t, [_c_int, _c_int] + [_c_int64] * 7
+    ),
+    "ms_deform_attn_backward_softmax_bin": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "ms_deform_attn_backward_softmax_rest": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "ms_deform_attn_backward_softmax": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr],
     ),
     "ms_deform_attn_forward_scatter_div": (
         _c_int,
@@ -154,6 +181,11 @@ class NativeLibrary:
             "backward_workspace": self.backward_workspace,
             "ms_deform_attn_backward_bin": self.ms_deform_attn_backward_bin,
             "ms_deform_attn_backward_rest": self.ms_deform_attn_backward_rest,
+            "ms_deform_attn_forward_softmax": self.ms_deform_attn_forward_softmax,
+            "ms_deform_attn_backward_softmax": self.ms_deform_attn_backward_softmax,
+            "backward_softmax_workspace": self.backward_softmax_workspace,
+            "ms_deform_attn_backward_softmax_bin": self.ms_deform_attn_backward_softmax_bin,
+            "ms_deform_attn_backward_softmax_rest": self.ms_deform_attn_backward_softmax_rest,
             "ms_deform_attn_forward_scatter_div": self.ms_deform_attn_forward_scatter_div,
             "ms_deform_attn_forward_scatter_div_cams": self.ms_deform_attn_forward_scatter_div_cams,
             "deformable_aggregation_forward_opt": self.deformable_aggregation_forward_opt,
@@ -201,6 +233,21 @@ class NativeLibrary:
         attention_weights, output, im2col_step: int,
     ) -> None:
         """Tensor-level forward with the reference export's argument order."""
+        self._forward_call("ms_deform_attn_forward", value, spatial_shapes, level_start_index,
+                           sampling_locations, attention_weights, output, im2col_step)
+
+    def ms_deform_attn_forward_softmax(
+        self, value, spatial_shapes, level_start_index, sampling_locations,
+        attention_logits, output, im2col_step: int,
+    ) -> None:
+        """Forward with the attention weights given as logits: each (b, q, m)
+        unit's weights are the softmax of its L*P logits (fused)."""
+        self._forward_call("ms_deform_attn_forward_softmax", value, spatial_shapes,
+                           level_start_index, sampling_locations, attention_logits, output,
+                           im2col_step)
+
+    def _forward_call(self, name, value, spatial_shapes, level_start_index, sampling_locations,
+                      attention_weights, output, im2col_step) -> None:
         import torch
 
         half = (torch.float32, torch.float16, torch.bfloat16)
@@ -223,14 +270,14 @@ class NativeLibrary:
         _check_shape(attention_weights, "attention_weights", (batch, queries, heads, levels, points))
         _check_shape(output, "out", (batch, queries, heads * channels))
         with torch.cuda.device(value.device):
-            rc = self._raw["ms_deform_attn_forward"](
+            rc = self._raw[name](
                 value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
                 level_start_index.data_ptr(), sampling_locations.data_ptr(),
                 attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
                 output.data_ptr(), batch, spatial, heads, channels, levels, queries, points,
                 int(im2col_step), self._stream(value),
             )
-        self._raise_on(rc, "ms_deform_attn_forward")
+        self._raise_on(rc, name)
 
     def ms_deform_attn_backward(
         self, value, spatial_shapes, level_start_index, sampling_locations,
@@ -243,6 +290,45 @@ class NativeLibrary:
         The tile-owned kernels' scratch comes from torch's caching allocator
         on the value's device.
         """
+        import torch
+
+        self._check_backward(value, spatial_shapes, level_start_index, sampling_locations,
+                             attention_weights, grad_output, grad_value, grad_sampling_locations,
+                             grad_attention_weights)
+        with torch.cuda.device(value.device):
+            workspace = self.backward_workspace(value, sampling_locations)
+            self._backward_call("ms_deform_attn_backward_ws", value, spatial_shapes,
+                                level_start_index, sampling_locations, attention_weights,
+                                grad_output, grad_value, grad_sampling_locations,
+                                grad_attention_weights, im2col_step, workspace,
+                                self._stream(value))
+
+    def ms_deform_attn_backward_softmax(
+        self, value, spatial_shapes, level_start_index, sampling_locations,
+        attention_logits, grad_output, grad_value, grad_sampling_locations,
+        grad_attention_logits, im2col_step: int,
+    ) -> None:
+        """Backward of :meth:`ms_deform_attn_forward_softmax`: the value,
+        location and logit gradients, all overwritten. Scratch (the softmax
+        probabilities and the binning) comes from torch's caching allocator."""
+        import torch
+
+        self._check_backward(value, spatial_shapes, level_start_index, sampling_locations,
+                             attention_logits, grad_output, grad_value, grad_sampling_locations,
+                             grad_attention_logits)
+        with torch.cuda.device(value.device):
+            workspace = self.backward_softmax_workspace(value, sampling_locations)
+            stream = self._stream(value)
+            for name in ("ms_deform_attn_backward_softmax_bin",
+                         "ms_deform_attn_backward_softmax_rest"):
+                self._backward_call(name, value, spatial_shapes, level_start_index,
+                                    sampling_locations, attention_logits, grad_output,
+                                    grad_value, grad_sampling_locations, grad_attention_logits,
+                                    im2col_step, workspace, stream)
+
+    def _check_backward(self, value, spatial_shapes, level_start_index, sampling_locations,
+                        attention_weights, grad_output, grad_value, grad_sampling_locations,
+                        grad_attention_weights) -> None:
         import torch
 
         half = (torch.float32, torch.float16, torch.bfloat16)
@@ -272,13 +358,6 @@ class NativeLibrary:
                      tuple(sampling_locations.shape))
         _check_shape(grad_attention_weights, "grad_attention_weights",
                      tuple(attention_weights.shape))
-        with torch.cuda.device(value.device):
-            workspace = self.backward_workspace(value, sampling_locations)
-            self._backward_call("ms_deform_attn_backward_ws", value, spatial_shapes,
-                                level_start_index, sampling_locations, attention_weights,
-                                grad_output, grad_value, grad_sampling_locations,
-                                grad_attention_weights, im2col_step, workspace,
-                                self._stream(value))
 
     def backward_workspace(self, value, sampling_locations):
         """Scratch of the tile-owned backward for these shapes (1 byte when the
@@ -290,6 +369,20 @@ class NativeLibrary:
                                    sampling_locations.shape[4])
         nbytes = self._raw["ms_deform_attn_backward_workspace_size"](
             _dtype_code(value.dtype), batch, spatial, heads, channels, levels, queries, points
+        )
+        return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=value.device)
+
+    def backward_softmax_workspace(self, value, sampling_locations):
+        """Scratch of the softmax backward for these shapes: the probabilities,
+        then the tile-owned kernels' scratch when the tile path applies."""
+        import torch
+
+        batch, spatial, heads, channels = value.shape
+        queries, levels, points = (sampling_locations.shape[1], sampling_locations.shape[3],
+                                   sampling_locations.shape[4])
+        nbytes = self._raw["ms_deform_attn_backward_softmax_workspace_size"](
+            _dtype_code(value.dtype), _dtype_code(sampling_locations.dtype), batch, spatial,
+            heads, channels, levels, queries, points,
         )
         return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=value.device)
 
@@ -342,6 +435,38 @@ class NativeLibrary:
                                 level_start_index, sampling_locations, attention_weights,
                                 grad_output, grad_value, grad_sampling_locations,
                                 grad_attention_weights, im2col_step, workspace,
+                                self._stream(value))
+
+    def ms_deform_attn_backward_softmax_bin(
+        self, value, spatial_shapes, level_start_index, sampling_locations, attention_logits,
+        grad_value, grad_sampling_locations, grad_attention_logits, im2col_step, workspace,
+        stream=None,
+    ) -> None:
+        """First part of the softmax backward (probabilities and binning; geometry
+        and logits only) on ``stream`` (default: the current stream)."""
+        import torch
+
+        st = stream if stream is not None else torch.cuda.current_stream(value.device)
+        with torch.cuda.device(value.device):
+            self._backward_call("ms_deform_attn_backward_softmax_bin", value, spatial_shapes,
+                                level_start_index, sampling_locations, attention_logits, None,
+                                grad_value, grad_sampling_locations, grad_attention_logits,
+                                im2col_step, workspace, st.cuda_stream)
+
+    def ms_deform_attn_backward_softmax_rest(
+        self, value, spatial_shapes, level_start_index, sampling_locations, attention_logits,
+        grad_output, grad_value, grad_sampling_locations, grad_attention_logits, im2col_step,
+        workspace,
+    ) -> None:
+        """Second part of the softmax backward on the current stream."""
+        import torch
+
+        _check(grad_output, "grad", (value.dtype,))
+        with torch.cuda.device(value.device):
+            self._backward_call("ms_deform_attn_backward_softmax_rest", value, spatial_shapes,
+                                level_start_index, sampling_locations, attention_logits,
+                                grad_output, grad_value, grad_sampling_locations,
+                                grad_attention_logits, im2col_step, workspace,
                                 self._stream(value))
 
     def ms_deform_attn_forward_scatter_div(

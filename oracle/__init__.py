@@ -18,6 +18,9 @@ Contents
                   (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa_kernel.muh:39-166);
                   used to pin msda_torch.py, not to check kernels directly.
   Makefile        builds msda_direct.c into oracle/build/libmsda_direct.so.
+  msda_softmax.py the operator with its weights given as logits (softmax over
+                  each query's L*P samples per head, then msda_torch); autograd
+                  and a closed-form logit gradient (tests/test_oracle_softmax.py).
 
 How each function is pinned (tests/test_oracle.py)
   * msda_torch vs msda_direct (two independent formulations) at float64;

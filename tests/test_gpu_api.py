@@ -214,6 +214,24 @@ def test_early_binning_matches_the_one_call_backward(monkeypatch):
         torch.testing.assert_close(b, c, rtol=1e-6, atol=1e-6)
 
 
+def test_no_binning_when_no_graph_is_recorded(monkeypatch):
+    """Under torch.no_grad() no backward can follow, so the forward starts no
+    binning even though its inputs require gradients (a tile-path shape)."""
+    monkeypatch.setenv("MUSPACE_EARLY_BINNING", "1")
+    inner = msda_module._native_extension()
+    spy = _NativeCallSpy(inner)
+    monkeypatch.setattr(msda_module, "_native_extension", lambda: spy)
+    tensors = _fixture(device=DEV, batch=1, queries=64, heads=2, embed_dims=32,
+                       levels=((8, 12),), points=4)
+    with torch.no_grad():
+        multi_scale_deformable_attn(*tensors, backend="hip")
+    assert [name for name, _ in spy.calls] == ["ms_deform_attn_forward"]
+    spy.calls.clear()
+    multi_scale_deformable_attn(*tensors, backend="hip")
+    assert [name for name, _ in spy.calls] == ["ms_deform_attn_backward_bin",
+                                               "ms_deform_attn_forward"]
+
+
 @pytest.mark.parametrize("embed_dims", [32, 3])
 def test_split_backward_entry_points_match_the_one_call(embed_dims):
     """ms_deform_attn_backward_bin on a second stream, then _rest on the main

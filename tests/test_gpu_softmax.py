@@ -1,0 +1,148 @@
+"""MSDA with the attention softmax fused in (ms_deform_attn_forward_softmax and
+its backward) on the GPU, against oracle/msda_softmax.py in float64 on the CPU.
+
+Cases: one step per unit (L*P <= the unit's tap lanes) and several steps (the
+online max/sum with rescaling), L*P not a power of two, channel counts 16, 32
+and 64 (row kernels, tile backward) and 8 (the standalone softmax with the
+generic forward and the atomic backward), 16-bit value storage, -inf logits,
+and the operator with its early binning on and off. Every gradient buffer
+starts as NaN, so an element the kernels fail to write fails the test.
+Tolerances: fp32 forward 1e-5, gradients 1e-4; 16-bit storage 2e-2.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import gpu_available
+from msda_testlib import level_starts
+from muspace_amd.runtime.native import load_native_module
+from oracle import msda_softmax
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not gpu_available(), reason="AMD GPU required"),
+]
+
+DEV = "cuda"
+LEVELS = ((20, 30), (10, 15), (5, 8), (3, 4))
+
+
+def _case(seed, *, batch=2, queries=70, heads=4, channels=32, levels=LEVELS, points=8):
+    g = torch.Generator().manual_seed(seed)
+    nv = sum(h * w for h, w in levels)
+    value = torch.randn(batch, nv, heads, channels, generator=g)
+    loc = torch.rand(batch, queries, heads, len(levels), points, 2, generator=g) * 1.2 - 0.1
+    logits = torch.randn(batch, queries, heads, len(levels), points, generator=g) * 2.0
+    grad = torch.randn(batch, queries, heads * channels, generator=g)
+    shapes = torch.tensor(levels, dtype=torch.int64)
+    return value, shapes, level_starts(levels), loc, logits, grad
+
+
+def _native(value, shapes, starts, loc, logits, grad, vdt=torch.float32, gdt=torch.float32):
+    lib = load_native_module()
+    v = value.to(DEV, vdt).contiguous()
+    lc, lg = loc.to(DEV, gdt).contiguous(), logits.to(DEV, gdt).contiguous()
+    sh, st = shapes.to(DEV), starts.to(DEV)
+    out = torch.empty((v.shape[0], lc.shape[1], v.shape[2] * v.shape[3]), dtype=vdt, device=DEV)
+    lib.ms_deform_attn_forward_softmax(v, sh, st, lc, lg, out, 64)
+    gv = torch.full(v.shape, float("nan"), device=DEV)
+    gl = torch.full(lc.shape, float("nan"), device=DEV)
+    glg = torch.full(lg.shape, float("nan"), device=DEV)
+    lib.ms_deform_attn_backward_softmax(v, sh, st, lc, lg, grad.to(DEV, vdt).contiguous(), gv,
+                                        gl, glg, 64)
+    torch.cuda.synchronize()
+    return [t.cpu().double() for t in (out, gv, gl, glg)]
+
+
+def _oracle(value, shapes, loc, logits, grad, vdt=torch.float32, gdt=torch.float32):
+    """The oracle on the inputs the kernels saw (rounded to their storage dtypes)."""
+    as_seen = lambda t, dt: t.to(dt).double()  # noqa: E731
+    out, gv, gl, glg = msda_softmax.forward_backward(
+        as_seen(value, vdt), shapes, as_seen(loc, gdt), as_seen(logits, gdt), as_seen(grad, vdt)
+    )
+    return [out, gv, gl, glg]
+
+
+def _assert_all(actual, expected, fwd_tol, bwd_tol, names=("out", "grad_value", "grad_loc",
+                                                           "grad_logits")):
+    for a, e, n in zip(actual, expected, names):
+        tol = fwd_tol if n == "out" else bwd_tol
+        torch.testing.assert_close(a, e, rtol=tol, atol=tol, msg=lambda m, n=n: f"{n}: {m}")
+
+
+@pytest.mark.parametrize(
+    "channels,levels,points",
+    [
+        (32, LEVELS, 8),        # one step per unit (L*P = 32)
+        (32, LEVELS, 32),       # two steps per unit: the online softmax rescales
+        (16, LEVELS, 8),
+        (64, LEVELS, 8),
+        (32, LEVELS[:3], 5),    # L*P = 15, not a power of two
+        (8, LEVELS, 4),         # standalone softmax, generic forward, atomic backward
+    ],
+)
+def test_fp32_forward_and_backward_match_the_oracle(channels, levels, points):
+    case = _case(channels * 100 + points, channels=channels, levels=levels, points=points)
+    value, shapes, starts, loc, logits, grad = case
+    _assert_all(_native(*case), _oracle(value, shapes, loc, logits, grad), 1e-5, 1e-4)
+
+
+@pytest.mark.parametrize("vdt,gdt", [(torch.bfloat16, torch.float32),
+                                     (torch.bfloat16, torch.bfloat16),
+                                     (torch.float16, torch.float16)])
+def test_16bit_storage_matches_the_oracle(vdt, gdt):
+    case = _case(7)
+    value, shapes, starts, loc, logits, grad = case
+    _assert_all(_native(*case, vdt=vdt, gdt=gdt),
+                _oracle(value, shapes, loc, logits, grad, vdt, gdt), 2e-2, 2e-2)
+
+
+def test_minus_infinity_logits():
+    """Masked samples get weight zero; a unit whose logits are all -inf gives
+    NaN, as torch.softmax does (its output row and its logit gradients)."""
+    case = list(_case(9))
+    logits = case[4]
+    logits[0, 3, 1, 0, :] = float("-inf")       # one level masked
+    logits[1, 5, 2, :, ::2] = float("-inf")     # every other point masked
+    logits[1, 6, 0] = float("-inf")             # the whole unit
+    value, shapes, starts, loc, logits, grad = case
+    out, gv, gl, glg = _native(*case)
+    e_out, e_gv, e_gl, e_glg = _oracle(value, shapes, loc, logits, grad)
+    torch.testing.assert_close(out, e_out, rtol=1e-5, atol=1e-5, equal_nan=True)
+    assert torch.isnan(out[1, 6, 0:32]).all() and torch.isfinite(out[1, 6, 32:]).all()
+    keep = torch.ones(logits.shape[:3], dtype=torch.bool)
+    keep[1, 6, 0] = False
+    torch.testing.assert_close(glg[keep], e_glg[keep], rtol=1e-4, atol=1e-4)
+    assert torch.isnan(glg[1, 6, 0]).all()
+
+
+@pytest.mark.parametrize("early", ["1", "0"])
+def test_operator_autograd_matches_the_oracle(early, monkeypatch):
+    from muspace_amd import clear_dispatch_report, get_last_dispatch_report
+    from muspace_amd.ops import multi_scale_deformable_attn_softmax
+
+    monkeypatch.setenv("MUSPACE_EARLY_BINNING", early)
+    value, shapes, starts, loc, logits, grad = _case(11)
+    v, lc, lg = (t.to(DEV).requires_grad_(True) for t in (value, loc, logits))
+    clear_dispatch_report()
+    out = multi_scale_deformable_attn_softmax(v, shapes.to(DEV), starts.to(DEV), lc, lg)
+    assert get_last_dispatch_report().selected_backend == "hip"
+    out.backward(grad.to(DEV))
+    expected = _oracle(value, shapes, loc, logits, grad)
+    actual = [out.detach().cpu().double()] + [t.grad.cpu().double() for t in (v, lc, lg)]
+    _assert_all(actual, expected, 1e-5, 1e-4)
+
+
+def test_fused_equals_softmax_then_operator():
+    """The fused forward against torch.softmax followed by the plain operator,
+    both on the GPU: only the order of float32 roundings differs."""
+    from muspace_amd.ops import (attention_softmax, multi_scale_deformable_attn,
+                                 multi_scale_deformable_attn_softmax)
+
+    value, shapes, starts, loc, logits, _ = _case(13, queries=300)
+    args = [t.to(DEV) for t in (value, shapes, starts, loc)]
+    fused = multi_scale_deformable_attn_softmax(*args, logits.to(DEV))
+    plain = multi_scale_deformable_attn(*args, attention_softmax(logits.to(DEV)))
+    torch.testing.assert_close(fused, plain, rtol=1e-5, atol=1e-6)
