@@ -24,7 +24,7 @@
 //                  lp_log2 | sample, wx1, wy1, attention weight} into their
 //                  tile (position: the top-left corner in the tile frame;
 //                  wx1, wy1: the bilinear fractions of the sample's tap).
-//   4. tile        persistent, one 1024-thread workgroup per CU, items taken
+//   4. tile        persistent, one 768-thread workgroup per CU, items taken
 //                  round-robin inside an XCD's share of the list: stage the
 //                  value tile in LDS, then for each batch of K records:
 //                  counting sort by top-left corner position in LDS, stage
@@ -50,7 +50,11 @@
 
 namespace msda {
 
-constexpr int kTileBlock = 512;          // tile kernel workgroup (8 wavefronts)
+// Tile kernel workgroup: 12 wavefronts, 3 per SIMD (at most 168 VGPRs; 512
+// threads, 2 per SIMD, left the VALU idle half the time: c2 tile kernel
+// 652 -> 622 us, c4 bf16 step 3419 -> 3236 us with K = 2304; 1024 threads
+// spill to scratch).
+constexpr int kTileBlock = 768;
 constexpr int kBinBlock = 256;           // binning workgroup
 constexpr int kMaxTilesPerSlab = 16384;  // LDS histogram of the binning kernels
 constexpr int kZeroList = 2048;          // tiles listed for zeroing per slab
@@ -94,12 +98,12 @@ constexpr uint32_t kTileIndexMask = 0xffffu;
 // planes, K sorted records and the position counts, offsets and order.
 template <typename VT, int C>
 struct TileCfg;
-template <> struct TileCfg<float, 16> { static constexpr int T = 16, K = 2048, CPL = 8; };
+template <> struct TileCfg<float, 16> { static constexpr int T = 16, K = 2304, CPL = 8; };
 template <> struct TileCfg<float, 32> { static constexpr int T = 13, K = 1536, CPL = 8; };
-template <> struct TileCfg<float, 64> { static constexpr int T = 8, K = 2048, CPL = 8; };
-template <> struct TileCfg<bf16_t, 16> { static constexpr int T = 16, K = 2048, CPL = 8; };
-template <> struct TileCfg<bf16_t, 32> { static constexpr int T = 13, K = 2048, CPL = 8; };
-template <> struct TileCfg<bf16_t, 64> { static constexpr int T = 9, K = 2048, CPL = 8; };
+template <> struct TileCfg<float, 64> { static constexpr int T = 8, K = 2304, CPL = 8; };
+template <> struct TileCfg<bf16_t, 16> { static constexpr int T = 16, K = 2304, CPL = 8; };
+template <> struct TileCfg<bf16_t, 32> { static constexpr int T = 13, K = 2304, CPL = 8; };
+template <> struct TileCfg<bf16_t, 64> { static constexpr int T = 9, K = 2304, CPL = 8; };
 template <> struct TileCfg<__half, 16> : TileCfg<bf16_t, 16> {};
 template <> struct TileCfg<__half, 32> : TileCfg<bf16_t, 32> {};
 template <> struct TileCfg<__half, 64> : TileCfg<bf16_t, 64> {};
