@@ -146,3 +146,45 @@ def test_fused_equals_softmax_then_operator():
     fused = multi_scale_deformable_attn_softmax(*args, logits.to(DEV))
     plain = multi_scale_deformable_attn(*args, attention_softmax(logits.to(DEV)))
     torch.testing.assert_close(fused, plain, rtol=1e-5, atol=1e-6)
+
+
+def _raw_backward_args(lib, value, shapes, starts, loc, logits, grad, gv, gl, glg):
+    from muspace_amd.runtime.native import DTYPE_F32
+
+    batch, spatial, heads, channels = value.shape
+    return [value.data_ptr(), DTYPE_F32, shapes.data_ptr(), starts.data_ptr(), loc.data_ptr(),
+            logits.data_ptr(), DTYPE_F32, grad.data_ptr(), gv.data_ptr(), gl.data_ptr(),
+            glg.data_ptr(), batch, spatial, heads, channels, shapes.shape[0], loc.shape[1],
+            loc.shape[4], 64]
+
+
+def test_allocating_backward_export_matches_the_workspace_calls():
+    """ms_deform_attn_backward_softmax (stream-ordered scratch) through the raw C-ABI
+    against _bin + _rest on a caller workspace, on the tile path (C = 32) and the
+    atomic path (C = 8)."""
+    lib = load_native_module()
+    for channels in (32, 8):
+        value, shapes, starts, loc, logits, grad = (t.to(DEV) for t in _case(21, channels=channels))
+        ref = [torch.empty(t.shape, device=DEV) for t in (value, loc, logits)]
+        lib.ms_deform_attn_backward_softmax(value, shapes, starts, loc, logits, grad, *ref, 64)
+        got = [torch.full(t.shape, float("nan"), device=DEV) for t in (value, loc, logits)]
+        args = _raw_backward_args(lib, value, shapes, starts, loc, logits, grad, *got)
+        rc = lib._raw["ms_deform_attn_backward_softmax"](
+            *args, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, lib._raw["muspace_last_error"]()
+        torch.cuda.synchronize()
+        for a, b in zip(got, ref):
+            torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-6)
+
+
+def test_softmax_backward_parts_need_a_workspace():
+    """The probabilities live in the workspace: _bin without one is MUSPACE_EINVAL
+    (checked on the host; nothing is launched)."""
+    lib = load_native_module()
+    value, shapes, starts, loc, logits, grad = (t.to(DEV) for t in _case(22))
+    bufs = [torch.empty(t.shape, device=DEV) for t in (value, loc, logits)]
+    args = _raw_backward_args(lib, value, shapes, starts, loc, logits, grad, *bufs)
+    rc = lib._raw["ms_deform_attn_backward_softmax_bin"](
+        *args, None, 0, torch.cuda.current_stream().cuda_stream)
+    assert rc == 1  # MUSPACE_EINVAL
+    assert b"workspace" in lib._raw["muspace_last_error"]()
