@@ -9,7 +9,8 @@ padding from the real thing pins nothing.
 Known answers come from the reference's own tests
 (/root/reference/tests/ops/test_multi_scale_deformable_attn.py:245-253,269-280,430-468);
 the rest are closed forms of bilinear sampling. The reference stores no golden
-tensors (SURVEY: tests/fixtures holds shape metadata only).
+tensors: its only fixture file for this path
+(/root/reference/tests/fixtures/bevformer_msda_shapes.yaml) holds shape metadata.
 """
 
 from __future__ import annotations
