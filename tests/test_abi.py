@@ -69,8 +69,9 @@ def _forward_args(**overrides):
         ({}, "null tensor pointer"),
     ],
 )
-def test_forward_validation_fails_before_any_launch(native_lib, overrides, message):
-    fn = native_lib.raw("ms_deform_attn_forward")
+@pytest.mark.parametrize("entry", ["ms_deform_attn_forward", "ms_deform_attn_forward_softmax"])
+def test_forward_validation_fails_before_any_launch(native_lib, overrides, message, entry):
+    fn = native_lib.raw(entry)
     rc = fn(*_forward_args(**overrides))
     assert rc != 0
     assert message in native_lib.last_error()
@@ -89,5 +90,75 @@ def test_backward_validation_fails_before_any_launch(native_lib):
     assert fn(*args) != 0
     assert "not divisible by im2col_step" in native_lib.last_error()
     args[-2] = 64
+    assert fn(*args) != 0
+    assert "null tensor pointer" in native_lib.last_error()
+
+
+def _backward_ws_args(**overrides):
+    args = dict(value=1, value_dtype=0, shapes=1, starts=1, loc=1, attn=1, geometry_dtype=0,
+                grad=1, grad_value=1, grad_loc=1, grad_attn=1, batch=2, spatial=4, heads=1,
+                channels=32, levels=1, queries=3, points=4, im2col_step=2, workspace=None,
+                workspace_bytes=0, stream=None)
+    args.update(overrides)
+    return list(args.values())
+
+
+@pytest.mark.parametrize("entry", ["ms_deform_attn_backward_softmax_bin",
+                                   "ms_deform_attn_backward_softmax_rest"])
+def test_softmax_backward_parts_require_a_workspace(native_lib, entry):
+    """The probabilities live at the head of the workspace: no or too small a
+    workspace is MUSPACE_EINVAL, checked before anything is launched (the plain
+    backward would fall back to atomics instead)."""
+    fn = native_lib.raw(entry)
+    assert fn(*_backward_ws_args()) == 1
+    assert "workspace" in native_lib.last_error()
+
+
+def test_softmax_workspace_size(native_lib):
+    size = native_lib.raw("ms_deform_attn_backward_softmax_workspace_size")
+    plain = native_lib.raw("ms_deform_attn_backward_workspace_size")
+    dims = (2, 4, 1, 32, 1, 3, 4)  # batch, spatial, heads, channels, levels, queries, points
+    probs = 2 * 3 * 1 * 4 * 4  # units * L*P * fp32, padded below to 256 bytes
+    assert size(0, 0, *dims) == 256 + plain(0, *dims)
+    assert size(0, 0, 2, 4, 1, 3, 1, 3, 4) == 256  # C = 3: no tile path, probabilities only
+    assert size(0, 0, 2, 4, 0, 32, 1, 3, 4) == 0  # invalid dims
+    assert size(0, 0, 2, 4, 1, 32, 1, 0, 4) == 0  # nothing sampled
+    assert probs < 256
+
+
+def _dfa_forward_args(**overrides):
+    args = dict(feat=1, shape=1, start=1, loc=1, weights=1, out=1, batch=1, cams=2, feat_n=10,
+                embeds=64, scales=2, anchors=3, pts=4, groups=8, stream=None)
+    args.update(overrides)
+    return list(args.values())
+
+
+@pytest.mark.parametrize(
+    ("overrides", "message"),
+    [
+        ({"groups": 9}, "num_groups must be in [1, 8]"),
+        ({"groups": 0}, "num_groups must be in [1, 8]"),
+        ({"embeds": 60}, "must be divisible by num_groups"),
+        ({"cams": 100, "scales": 3}, "num_cams * num_scale must be at most 256"),
+        ({"anchors": -1}, "invalid dims"),
+        ({"out": None}, "null tensor pointer"),
+    ],
+)
+@pytest.mark.parametrize("entry", ["deformable_aggregation_forward_opt",
+                                   "deformable_aggregation_forward_base"])
+def test_dfa_forward_validation_fails_before_any_launch(native_lib, overrides, message, entry):
+    fn = native_lib.raw(entry)
+    assert fn(*_dfa_forward_args(**overrides)) != 0
+    assert message in native_lib.last_error()
+
+
+@pytest.mark.parametrize("entry", ["deformable_aggregation_backward_opt",
+                                   "deformable_aggregation_backward_base"])
+def test_dfa_backward_validation_fails_before_any_launch(native_lib, entry):
+    fn = native_lib.raw(entry)
+    args = [1] * 9 + [1, 2, 10, 64, 2, 3, 4, 9, None]  # 9 groups
+    assert fn(*args) != 0
+    assert "num_groups must be in [1, 8]" in native_lib.last_error()
+    args = [1] * 5 + [None] + [1] * 3 + [1, 2, 10, 64, 2, 3, 4, 8, None]  # grad_output NULL
     assert fn(*args) != 0
     assert "null tensor pointer" in native_lib.last_error()
