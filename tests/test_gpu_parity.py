@@ -147,6 +147,40 @@ def test_small_shapes_match_oracle(native_lib, case, dtypes):
     _assert_close(ga, o_ga, btol, "grad_attention_weights")
 
 
+# Binning-boundary shapes, small enough for the full oracle: several binning
+# chunks per (b, m) slab (chunk = max(256, 4096 / pow2(L*P)) queries) with a
+# ragged last chunk that also ends inside a sub-chunk (2048 / pow2(L*P)
+# queries), and L*P = 3, 5, 6 so that padded sample slots sit inside every
+# sub-chunk. Shapes: L*P = 3 -> 1024-query chunks, 512-query sub-chunks,
+# 2600 = 2 x 1024 + 552; L*P = 5 -> 512 and 256, 1300 = 2 x 512 + 276;
+# L*P = 6 on C = 16 and 64 tiles.
+MEDIUM = [
+    (1, 2600, 2, 32, ((20, 30), (10, 15), (5, 8)), 1),
+    (2, 1300, 2, 32, ((16, 24),), 5),
+    (1, 1100, 2, 16, ((12, 18), (6, 9), (3, 5)), 2),
+    (1, 1100, 2, 64, ((12, 18), (6, 9), (3, 5)), 2),
+]
+
+
+@pytest.mark.parametrize("dtypes", DTYPES[:2], ids=lambda d: f"{d[0]}-{d[1]}".replace("torch.", ""))
+@pytest.mark.parametrize("case", MEDIUM, ids=_id)
+def test_binning_chunk_boundaries_match_oracle(native_lib, case, dtypes):
+    value_dtype, geometry_dtype = dtypes
+    print(f"[parity] medium {_id(case)} {value_dtype}", flush=True)
+    t, grad = small_case(sum(case[:4]), *case)
+    out = run_forward(native_lib, t, value_dtype, geometry_dtype)
+    gv, gl, ga = run_backward(native_lib, t, grad, value_dtype, geometry_dtype)
+    torch.cuda.synchronize()
+    o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
+        *oracle_inputs(t, value_dtype, geometry_dtype), grad.to(value_dtype).float()
+    )
+    ftol, btol = TOL[value_dtype]
+    _assert_close(out, o_out, ftol, "output")
+    _assert_close(gv, o_gv, btol, "grad_value")
+    _assert_close(gl, o_gl, btol, "grad_sampling_locations")
+    _assert_close(ga, o_ga, btol, "grad_attention_weights")
+
+
 def test_im2col_step_chunking_has_no_numeric_effect(native_lib):
     t, grad = small_case(5, 4, 9, 8, 32, ((6, 7), (3, 4)), 4)
     out_a = run_forward(native_lib, t, torch.float32, torch.float32, im2col_step=64)
