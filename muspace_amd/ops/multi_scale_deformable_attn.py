@@ -215,6 +215,9 @@ class _NativeMSDAFunction(torch.autograd.Function):
         output = value_arg.new_empty(
             (value_arg.size(0), sampling_arg.size(1), value_arg.size(2) * value_arg.size(3))
         )
+        # every tensor is checked before the first launch (the binning below
+        # runs before the forward's own launch)
+        ext.check_forward(value_arg, spatial_arg, start_arg, sampling_arg, attn_arg, output)
         ctx.binned = None
         if early_binning and any(ctx.needs_input_grad[i] for i in (0, 3, 4)):
             ctx.binned = _start_binning(ext, value_arg, spatial_arg, start_arg, sampling_arg,

@@ -9,9 +9,13 @@ on tensors of torch's ``cuda`` device type under a HIP build of torch.
 Differences from the reference, both deliberate:
   * the report history is bounded (``MAX_REPORTS`` most recent reports) where
     the reference appends to an unbounded list (kernel_dispatch.py:43,49);
-  * ``auto`` on a ROCm tensor without the native library is an error rather
-    than a silent switch to the PyTorch path: the HIP kernels are the product
-    on that device, so a missing library must be visible.
+  * ``auto`` on a ROCm tensor without the native library is an error by
+    default rather than a silent switch to the PyTorch path: the HIP kernels
+    are the product on that device, so a missing library must be visible.
+    ``MUSPACE_AUTO_FALLBACK=1`` restores the reference's behaviour
+    (kernel_dispatch.py:94-100): ``auto`` then selects the PyTorch path with
+    the unavailability as the recorded reason, for callers such as patched
+    mmcv models that prefer degrading to failing.
 """
 
 from __future__ import annotations
@@ -32,6 +36,7 @@ NATIVE_BACKEND = "hip"
 NATIVE_ALIASES = frozenset({"hip", "musa"})
 MAX_REPORTS = 4096
 LOG_ENV = "MUSPACE_DISPATCH_LOG"
+AUTO_FALLBACK_ENV = "MUSPACE_AUTO_FALLBACK"
 
 
 @dataclass(frozen=True)
@@ -63,8 +68,12 @@ _last_dispatch_report: DispatchReport | None = None
 _dispatch_reports: deque[DispatchReport] = deque(maxlen=MAX_REPORTS)
 
 
+def _env_flag(name: str) -> bool:
+    return os.environ.get(name, "").strip().lower() in {"1", "true", "yes", "on"}
+
+
 def _log_enabled() -> bool:
-    return os.environ.get(LOG_ENV, "").strip().lower() in {"1", "true", "yes", "on"}
+    return _env_flag(LOG_ENV)
 
 
 def record_dispatch_report(report: DispatchReport) -> DispatchReport:
@@ -118,6 +127,10 @@ def explain_dispatch(
 
     if is_rocm_tensor(value):
         if not native_available:
+            if _env_flag(AUTO_FALLBACK_ENV):
+                return DispatchDecision(
+                    "reference", device,
+                    "HIP backend is unavailable; falling back to PyTorch reference")
             return DispatchDecision("error", device, unavailable)
         return DispatchDecision(NATIVE_BACKEND, device, "ROCm tensor selects native HIP backend")
 

@@ -138,9 +138,21 @@ def _dtype_code(dtype) -> int:
         raise RuntimeError(f"unsupported dtype {dtype}") from None
 
 
-def _check(tensor, name: str, dtypes) -> None:
-    if not getattr(tensor, "is_cuda", False):
+def _is_device_tensor(tensor) -> bool:
+    """A tensor in GPU memory (torch's ``cuda`` device type on a ROCm build)."""
+    return bool(getattr(tensor, "is_cuda", False))
+
+
+def _check(tensor, name: str, dtypes, device=None) -> None:
+    """Device, dtype and contiguity of one tensor argument (the reference's
+    ``check_musa_contiguous``, csrc/ffi/tensor_utils.hpp:13-38); ``device``,
+    when given, is the device every argument of the call must share."""
+    if tensor is None:
+        raise RuntimeError(f"{name} is required")
+    if not _is_device_tensor(tensor):
         raise RuntimeError(f"{name} must be a ROCm device tensor, got device {tensor.device}")
+    if device is not None and tensor.device != device:
+        raise RuntimeError(f"{name} is on {tensor.device}, expected {device} (the value's device)")
     if tensor.dtype not in dtypes:
         allowed = ", ".join(str(d).replace("torch.", "") for d in dtypes)
         raise RuntimeError(f"{name} must be {allowed}, got {str(tensor.dtype).replace('torch.', '')}")
@@ -176,6 +188,8 @@ class NativeLibrary:
                 "rebuild it with `python -m muspace_amd.build`"
             )
         self._bound: dict[str, Callable[..., Any]] = {
+            "check_forward": self.check_forward,
+            "check_backward": self.check_backward,
             "ms_deform_attn_forward": self.ms_deform_attn_forward,
             "ms_deform_attn_backward": self.ms_deform_attn_backward,
             "backward_workspace": self.backward_workspace,
@@ -246,20 +260,31 @@ class NativeLibrary:
                            level_start_index, sampling_locations, attention_logits, output,
                            im2col_step)
 
-    def _forward_call(self, name, value, spatial_shapes, level_start_index, sampling_locations,
-                      attention_weights, output, im2col_step) -> None:
+    def check_forward(self, value, spatial_shapes, level_start_index, sampling_locations,
+                      attention_weights, output=None) -> tuple[int, ...]:
+        """Validate the forward's tensors without launching anything.
+
+        Every tensor must be a contiguous ROCm tensor on the value's device
+        with the dtype the kernels read, and the shapes must agree with
+        ``value`` and ``spatial_shapes`` -- the reference checks all of them
+        before its first launch (ms_deform_attn_musa.mu:514-522,
+        csrc/ffi/tensor_utils.hpp:13-38). ``output`` may be None (the binning
+        part of the backward has none). Raises RuntimeError; returns
+        (batch, spatial, heads, channels, levels, queries, points).
+        """
         import torch
 
-        half = (torch.float32, torch.float16, torch.bfloat16)
-        _check(value, "value", half)
-        _check(spatial_shapes, "spatial_shapes", (torch.int64,))
-        _check(level_start_index, "level_start_index", (torch.int64,))
+        _check(value, "value", (torch.float32, torch.float16, torch.bfloat16))
+        dev = value.device
+        _check(spatial_shapes, "spatial_shapes", (torch.int64,), dev)
+        _check(level_start_index, "level_start_index", (torch.int64,), dev)
         geom = (torch.float32,) if value.dtype == torch.float32 else (torch.float32, value.dtype)
-        _check(sampling_locations, "sampling_locations", geom)
-        _check(attention_weights, "attention_weights", (sampling_locations.dtype,))
-        _check(output, "out", (value.dtype,))
+        _check(sampling_locations, "sampling_locations", geom, dev)
+        _check(attention_weights, "attention_weights", (sampling_locations.dtype,), dev)
         if value.dim() != 4 or sampling_locations.dim() != 6:
             raise RuntimeError("value must be 4-D and sampling_locations 6-D")
+        if spatial_shapes.dim() != 2:
+            raise RuntimeError("spatial_shapes must be 2-D [num_levels, 2]")
         batch, spatial, heads, channels = value.shape
         levels = spatial_shapes.shape[0]
         queries, points = sampling_locations.shape[1], sampling_locations.shape[4]
@@ -268,7 +293,43 @@ class NativeLibrary:
         _check_shape(sampling_locations, "sampling_locations",
                      (batch, queries, heads, levels, points, 2))
         _check_shape(attention_weights, "attention_weights", (batch, queries, heads, levels, points))
-        _check_shape(output, "out", (batch, queries, heads * channels))
+        if output is not None:
+            _check(output, "out", (value.dtype,), dev)
+            _check_shape(output, "out", (batch, queries, heads * channels))
+        return batch, spatial, heads, channels, levels, queries, points
+
+    def check_backward(self, value, spatial_shapes, level_start_index, sampling_locations,
+                       attention_weights, grad_output, grad_value, grad_sampling_locations,
+                       grad_attention_weights) -> tuple[int, ...]:
+        """Validate the backward's tensors (as :meth:`check_forward`, plus
+        grad_output in the value's dtype and three float32 gradients of the
+        inputs' shapes). ``grad_output`` is None for the binning part, which
+        does not read it. Raises RuntimeError; returns the dims."""
+        import torch
+
+        dims = self.check_forward(value, spatial_shapes, level_start_index, sampling_locations,
+                                  attention_weights)
+        batch, _, heads, channels, _, queries, _ = dims
+        dev = value.device
+        if grad_output is not None:
+            _check(grad_output, "grad", (value.dtype,), dev)
+            _check_shape(grad_output, "grad", (batch, queries, heads * channels))
+        for tensor, name, like in ((grad_value, "grad_value", value),
+                                   (grad_sampling_locations, "grad_sampling_locations",
+                                    sampling_locations),
+                                   (grad_attention_weights, "grad_attention_weights",
+                                    attention_weights)):
+            _check(tensor, name, (torch.float32,), dev)
+            _check_shape(tensor, name, tuple(like.shape))
+        return dims
+
+    def _forward_call(self, name, value, spatial_shapes, level_start_index, sampling_locations,
+                      attention_weights, output, im2col_step) -> None:
+        import torch
+
+        batch, spatial, heads, channels, levels, queries, points = self.check_forward(
+            value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+            output)
         with torch.cuda.device(value.device):
             rc = self._raw[name](
                 value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
@@ -292,9 +353,9 @@ class NativeLibrary:
         """
         import torch
 
-        self._check_backward(value, spatial_shapes, level_start_index, sampling_locations,
-                             attention_weights, grad_output, grad_value, grad_sampling_locations,
-                             grad_attention_weights)
+        self.check_backward(value, spatial_shapes, level_start_index, sampling_locations,
+                            attention_weights, grad_output, grad_value, grad_sampling_locations,
+                            grad_attention_weights)
         with torch.cuda.device(value.device):
             workspace = self.backward_workspace(value, sampling_locations)
             self._backward_call("ms_deform_attn_backward_ws", value, spatial_shapes,
@@ -313,9 +374,9 @@ class NativeLibrary:
         probabilities and the binning) comes from torch's caching allocator."""
         import torch
 
-        self._check_backward(value, spatial_shapes, level_start_index, sampling_locations,
-                             attention_logits, grad_output, grad_value, grad_sampling_locations,
-                             grad_attention_logits)
+        self.check_backward(value, spatial_shapes, level_start_index, sampling_locations,
+                            attention_logits, grad_output, grad_value, grad_sampling_locations,
+                            grad_attention_logits)
         with torch.cuda.device(value.device):
             workspace = self.backward_softmax_workspace(value, sampling_locations)
             stream = self._stream(value)
@@ -326,65 +387,50 @@ class NativeLibrary:
                                     grad_value, grad_sampling_locations, grad_attention_logits,
                                     im2col_step, workspace, stream)
 
-    def _check_backward(self, value, spatial_shapes, level_start_index, sampling_locations,
-                        attention_weights, grad_output, grad_value, grad_sampling_locations,
-                        grad_attention_weights) -> None:
-        import torch
-
-        half = (torch.float32, torch.float16, torch.bfloat16)
-        _check(value, "value", half)
-        _check(spatial_shapes, "spatial_shapes", (torch.int64,))
-        _check(level_start_index, "level_start_index", (torch.int64,))
-        geom = (torch.float32,) if value.dtype == torch.float32 else (torch.float32, value.dtype)
-        _check(sampling_locations, "sampling_locations", geom)
-        _check(attention_weights, "attention_weights", (sampling_locations.dtype,))
-        _check(grad_output, "grad", (value.dtype,))
-        _check(grad_value, "grad_value", (torch.float32,))
-        _check(grad_sampling_locations, "grad_sampling_locations", (torch.float32,))
-        _check(grad_attention_weights, "grad_attention_weights", (torch.float32,))
-        if value.dim() != 4 or sampling_locations.dim() != 6:
-            raise RuntimeError("value must be 4-D and sampling_locations 6-D")
+    def _workspace_bytes(self, value, sampling_locations, softmax: bool) -> int:
         batch, spatial, heads, channels = value.shape
-        levels = spatial_shapes.shape[0]
-        queries, points = sampling_locations.shape[1], sampling_locations.shape[4]
-        _check_shape(spatial_shapes, "spatial_shapes", (levels, 2))
-        _check_shape(level_start_index, "level_start_index", (levels,))
-        _check_shape(sampling_locations, "sampling_locations",
-                     (batch, queries, heads, levels, points, 2))
-        _check_shape(attention_weights, "attention_weights", (batch, queries, heads, levels, points))
-        _check_shape(grad_output, "grad", (batch, queries, heads * channels))
-        _check_shape(grad_value, "grad_value", tuple(value.shape))
-        _check_shape(grad_sampling_locations, "grad_sampling_locations",
-                     tuple(sampling_locations.shape))
-        _check_shape(grad_attention_weights, "grad_attention_weights",
-                     tuple(attention_weights.shape))
+        queries, levels, points = (sampling_locations.shape[1], sampling_locations.shape[3],
+                                   sampling_locations.shape[4])
+        if softmax:
+            return int(self._raw["ms_deform_attn_backward_softmax_workspace_size"](
+                _dtype_code(value.dtype), _dtype_code(sampling_locations.dtype), batch, spatial,
+                heads, channels, levels, queries, points))
+        return int(self._raw["ms_deform_attn_backward_workspace_size"](
+            _dtype_code(value.dtype), batch, spatial, heads, channels, levels, queries, points))
 
     def backward_workspace(self, value, sampling_locations):
         """Scratch of the tile-owned backward for these shapes (1 byte when the
         shape takes the atomic fallback)."""
         import torch
 
-        batch, spatial, heads, channels = value.shape
-        queries, levels, points = (sampling_locations.shape[1], sampling_locations.shape[3],
-                                   sampling_locations.shape[4])
-        nbytes = self._raw["ms_deform_attn_backward_workspace_size"](
-            _dtype_code(value.dtype), batch, spatial, heads, channels, levels, queries, points
-        )
-        return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=value.device)
+        nbytes = self._workspace_bytes(value, sampling_locations, softmax=False)
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=value.device)
 
     def backward_softmax_workspace(self, value, sampling_locations):
         """Scratch of the softmax backward for these shapes: the probabilities,
         then the tile-owned kernels' scratch when the tile path applies."""
         import torch
 
-        batch, spatial, heads, channels = value.shape
-        queries, levels, points = (sampling_locations.shape[1], sampling_locations.shape[3],
-                                   sampling_locations.shape[4])
-        nbytes = self._raw["ms_deform_attn_backward_softmax_workspace_size"](
-            _dtype_code(value.dtype), _dtype_code(sampling_locations.dtype), batch, spatial,
-            heads, channels, levels, queries, points,
-        )
-        return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=value.device)
+        nbytes = self._workspace_bytes(value, sampling_locations, softmax=True)
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=value.device)
+
+    def _check_split(self, value, spatial_shapes, level_start_index, sampling_locations,
+                     attention_weights, grad_output, grad_value, grad_sampling_locations,
+                     grad_attention_weights, workspace, softmax: bool) -> None:
+        """Checks of one part of a backward split in two (binning, rest): every
+        tensor as :meth:`check_backward`, and a workspace of at least the size
+        the shapes need, so both parts take the same path (a smaller one
+        would make the binning skip the tile path while the rest expects it)."""
+        import torch
+
+        self.check_backward(value, spatial_shapes, level_start_index, sampling_locations,
+                            attention_weights, grad_output, grad_value, grad_sampling_locations,
+                            grad_attention_weights)
+        _check(workspace, "workspace", (torch.uint8,), value.device)
+        need = self._workspace_bytes(value, sampling_locations, softmax)
+        if workspace.numel() < need:
+            raise RuntimeError(f"workspace holds {workspace.numel()} bytes, these shapes need "
+                               f"{need}")
 
     def _backward_call(self, name, value, spatial_shapes, level_start_index, sampling_locations,
                        attention_weights, grad_output, grad_value, grad_sampling_locations,
@@ -403,22 +449,35 @@ class NativeLibrary:
         )
         self._raise_on(rc, name)
 
+    def _split_part(self, name, softmax, value, spatial_shapes, level_start_index,
+                    sampling_locations, attention_weights, grad_output, grad_value,
+                    grad_sampling_locations, grad_attention_weights, im2col_step, workspace,
+                    stream) -> None:
+        import torch
+
+        self._check_split(value, spatial_shapes, level_start_index, sampling_locations,
+                          attention_weights, grad_output, grad_value, grad_sampling_locations,
+                          grad_attention_weights, workspace, softmax)
+        st = stream if stream is not None else torch.cuda.current_stream(value.device)
+        with torch.cuda.device(value.device):
+            self._backward_call(name, value, spatial_shapes, level_start_index,
+                                sampling_locations, attention_weights, grad_output, grad_value,
+                                grad_sampling_locations, grad_attention_weights, im2col_step,
+                                workspace, st.cuda_stream)
+
     def ms_deform_attn_backward_bin(
         self, value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
         grad_value, grad_sampling_locations, grad_attention_weights, im2col_step, workspace,
         stream=None,
     ) -> None:
         """First part of the backward (binning; geometry only) on ``stream``
-        (default: the current stream). Inputs were checked by the caller, which
-        passes the same tensors to :meth:`ms_deform_attn_backward_rest`."""
-        import torch
-
-        st = stream if stream is not None else torch.cuda.current_stream(value.device)
-        with torch.cuda.device(value.device):
-            self._backward_call("ms_deform_attn_backward_bin", value, spatial_shapes,
-                                level_start_index, sampling_locations, attention_weights, None,
-                                grad_value, grad_sampling_locations, grad_attention_weights,
-                                im2col_step, workspace, st.cuda_stream)
+        (default: the current stream). Every tensor is checked before the
+        launch; :meth:`ms_deform_attn_backward_rest` on the same workspace and
+        gradients must follow it on a stream ordered after this one."""
+        self._split_part("ms_deform_attn_backward_bin", False, value, spatial_shapes,
+                         level_start_index, sampling_locations, attention_weights, None,
+                         grad_value, grad_sampling_locations, grad_attention_weights,
+                         im2col_step, workspace, stream)
 
     def ms_deform_attn_backward_rest(
         self, value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
@@ -427,15 +486,10 @@ class NativeLibrary:
     ) -> None:
         """Second part of the backward on the current stream, after the binning
         of the same workspace (ordered by the caller)."""
-        import torch
-
-        _check(grad_output, "grad", (value.dtype,))
-        with torch.cuda.device(value.device):
-            self._backward_call("ms_deform_attn_backward_rest", value, spatial_shapes,
-                                level_start_index, sampling_locations, attention_weights,
-                                grad_output, grad_value, grad_sampling_locations,
-                                grad_attention_weights, im2col_step, workspace,
-                                self._stream(value))
+        self._split_part("ms_deform_attn_backward_rest", False, value, spatial_shapes,
+                         level_start_index, sampling_locations, attention_weights, grad_output,
+                         grad_value, grad_sampling_locations, grad_attention_weights,
+                         im2col_step, workspace, None)
 
     def ms_deform_attn_backward_softmax_bin(
         self, value, spatial_shapes, level_start_index, sampling_locations, attention_logits,
@@ -444,14 +498,10 @@ class NativeLibrary:
     ) -> None:
         """First part of the softmax backward (probabilities and binning; geometry
         and logits only) on ``stream`` (default: the current stream)."""
-        import torch
-
-        st = stream if stream is not None else torch.cuda.current_stream(value.device)
-        with torch.cuda.device(value.device):
-            self._backward_call("ms_deform_attn_backward_softmax_bin", value, spatial_shapes,
-                                level_start_index, sampling_locations, attention_logits, None,
-                                grad_value, grad_sampling_locations, grad_attention_logits,
-                                im2col_step, workspace, st.cuda_stream)
+        self._split_part("ms_deform_attn_backward_softmax_bin", True, value, spatial_shapes,
+                         level_start_index, sampling_locations, attention_logits, None,
+                         grad_value, grad_sampling_locations, grad_attention_logits,
+                         im2col_step, workspace, stream)
 
     def ms_deform_attn_backward_softmax_rest(
         self, value, spatial_shapes, level_start_index, sampling_locations, attention_logits,
@@ -459,15 +509,10 @@ class NativeLibrary:
         workspace,
     ) -> None:
         """Second part of the softmax backward on the current stream."""
-        import torch
-
-        _check(grad_output, "grad", (value.dtype,))
-        with torch.cuda.device(value.device):
-            self._backward_call("ms_deform_attn_backward_softmax_rest", value, spatial_shapes,
-                                level_start_index, sampling_locations, attention_logits,
-                                grad_output, grad_value, grad_sampling_locations,
-                                grad_attention_logits, im2col_step, workspace,
-                                self._stream(value))
+        self._split_part("ms_deform_attn_backward_softmax_rest", True, value, spatial_shapes,
+                         level_start_index, sampling_locations, attention_logits, grad_output,
+                         grad_value, grad_sampling_locations, grad_attention_logits,
+                         im2col_step, workspace, None)
 
     def ms_deform_attn_forward_scatter_div(
         self, value, spatial_shapes, level_start_index, sampling_locations,

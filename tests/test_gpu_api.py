@@ -47,7 +47,8 @@ class _NativeCallSpy:
         target = getattr(self._inner, name)
 
         def recorded(*args, **kwargs):
-            if name != "backward_workspace":  # a size query, not a kernel entry point
+            # size queries and argument checks are not kernel entry points
+            if name not in {"backward_workspace", "check_forward", "check_backward"}:
                 self.calls.append((name, [getattr(arg, "dtype", None) for arg in args]))
             return target(*args, **kwargs)
 

@@ -199,6 +199,21 @@ def test_rocm_tensor_without_library_is_an_error_not_a_fallback(monkeypatch):
     assert forced.backend == "hip"
 
 
+def test_auto_fallback_env_restores_the_reference_policy(monkeypatch):
+    """MUSPACE_AUTO_FALLBACK=1: auto on a ROCm tensor without the library takes
+    the PyTorch path with the reason recorded (reference kernel_dispatch.py:94-100);
+    a forced native backend still fails."""
+    monkeypatch.setattr(dispatch_module, "is_rocm_tensor", lambda tensor: True)
+    monkeypatch.setenv("MUSPACE_AUTO_FALLBACK", "1")
+    decision = dispatch_module.explain_dispatch(torch.zeros(1), backend="auto",
+                                                native_available=False)
+    assert decision.backend == "reference"
+    assert decision.reason == "HIP backend is unavailable; falling back to PyTorch reference"
+    forced = dispatch_module.explain_dispatch(torch.zeros(1), backend="hip",
+                                              native_available=False)
+    assert forced.backend == "error"
+
+
 def test_spatial_shape_dtype_is_validated():
     value, spatial_shapes, level_start_index, sampling_locations, attention_weights = _fixture()
     with pytest.raises(TypeError, match="spatial_shapes must be int64"):
