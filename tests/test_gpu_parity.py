@@ -258,6 +258,29 @@ def test_add_one_smoke(native_lib):
 
 # ------------------------------------------------------ BASELINE configs ---
 
+
+def test_c0_full_oracle(native_lib):
+    """BASELINE c0 (bs 1, 1000 queries, levels 32x32..4x4, 4 points, float32;
+    locations U(-0.05, 1.05), so samples leave the levels): the HIP forward
+    against the oracle on every query at 1e-5, and the backward (c0 names the
+    forward only; the gradients are checked as well, at 1e-4)."""
+    cfg = CONFIGS["c0"]
+    print(f"[parity] c0 bs={cfg.batch} nq={cfg.queries}", flush=True)
+    t = make_inputs(cfg, value_dtype=torch.float32)
+    grad = t.pop("grad_output")
+    out = run_forward(native_lib, t, torch.float32, torch.float32)
+    gv, gl, ga = run_backward(native_lib, t, grad, torch.float32, torch.float32)
+    torch.cuda.synchronize()
+    o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
+        t["value"], t["spatial_shapes"], t["sampling_locations"], t["attention_weights"], grad)
+    _assert_close(out, o_out, 1e-5, "c0 output")
+    _assert_close(gv, o_gv, 1e-4, "c0 grad_value")
+    _assert_close(gl, o_gl, 1e-4, "c0 grad_sampling_locations")
+    _assert_close(ga, o_ga, 1e-4, "c0 grad_attention_weights")
+    outside = ((t["sampling_locations"] < 0) | (t["sampling_locations"] > 1)).any(-1)
+    assert outside.float().mean() > 0.05  # the zero-padding path is exercised
+
+
 FULL = [
     ("c1", torch.float32, torch.float32),
     ("c2", torch.float32, torch.float32),
@@ -265,6 +288,7 @@ FULL = [
     ("c4", torch.bfloat16, torch.float32),
     ("c4", torch.float16, torch.float32),
     ("bevformer-1l", torch.float32, torch.float32),
+    ("bevformer-1l", torch.bfloat16, torch.float32),
 ]
 SUBSET = 48  # queries per config checked against the oracle
 
