@@ -32,6 +32,7 @@ import argparse
 import json
 import os
 import platform
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -48,6 +49,7 @@ from muspace_amd.workloads import (  # noqa: E402
     algorithmic_bytes,
     backward_rest_bytes,
     make_inputs,
+    make_published_case,
     dfa_algorithmic_bytes,
     make_dfa_inputs,
     make_sca_inputs,
@@ -131,13 +133,19 @@ class Step:
         mark("rest1", main)
 
 
-def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True) -> dict:
-    """Time `steps` steps after `warmup`. Inside the timed region HIP events sit
+def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True,
+               repeats: int = 5) -> dict:
+    """Time exactly `steps` steps after `warmup`, as `repeats` back-to-back
+    repeats of steps // repeats steps (the remainder goes to the first
+    repeats), each bracketed by device synchronisation and HIP events on the
+    main stream; ms_per_step is the median of the repeats' per-step means
+    (the reference's protocol, /root/reference/benchmarks/_harness.py:226-260),
+    with the overall mean beside it. Inside the timed region HIP events sit
     only around the rest of the backward (the roofline's kernel) on the main
-    stream: each pair of events costs about 10 us a step, and a pair around the
-    forward also delays its overlap with the binning. The forward's, the
-    binning's and the allocation's durations come from a separate pass of a few
-    steps. bwd_ms adds the binning and the rest."""
+    stream: each pair of events costs about 10 us a step, and a pair around
+    the forward also delays its overlap with the binning. The forward's, the
+    binning's and the allocation's durations come from a separate pass of a
+    few steps. bwd_ms adds the binning and the rest."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         step.run()
@@ -153,20 +161,30 @@ def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True) -> 
         return mark
 
     timed = marker({"rest0", "rest1"})
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    repeats = max(1, min(repeats, steps))
+    counts = [steps // repeats + (1 if r < steps % repeats else 0) for r in range(repeats)]
+    samples, total_ms = [], 0.0
     t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(steps):
-        if per_kernel:
-            marks.append({})
-            step.run(timed)
-        else:
-            step.run()
-    end.record(stream)
-    torch.cuda.synchronize()
+    for n in counts:
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(n):
+            if per_kernel:
+                marks.append({})
+                step.run(timed)
+            else:
+                step.run()
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end)
+        samples.append(ms / n)
+        total_ms += ms
     wall = time.perf_counter() - t0
-    res = {"ms_per_step": start.elapsed_time(end) / steps, "wall_ms_per_step": wall * 1e3 / steps}
+    res = {"ms_per_step": statistics.median(samples), "mean_ms_per_step": total_ms / steps,
+           "repeat_ms_per_step": [round(x, 4) for x in samples],
+           "wall_ms_per_step": wall * 1e3 / steps}
     if per_kernel:
         def avg(a, b):
             return sum(m[a].elapsed_time(m[b]) for m in marks) / len(marks)
@@ -182,6 +200,27 @@ def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True) -> 
         res["zero_ms"] = avg("alloc0", "alloc1")
         res["bwd_ms"] = res["bin_ms"] + res["rest_ms"]
     return res
+
+
+def harness_ms(fn, warmup: int = 20, iterations: int = 100, repeats: int = 5) -> float:
+    """The reference's protocol (/root/reference/benchmarks/_harness.py:226-260):
+    `warmup` calls, then `repeats` repeats of `iterations` calls between HIP
+    events on the current stream; the median of the repeats' per-call ms."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(repeats):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(iterations):
+            fn()
+        end.record(stream)
+        end.synchronize()
+        samples.append(start.elapsed_time(end) / iterations)
+    return statistics.median(samples)
 
 
 def _event_ms(fn, steps: int, warmup: int) -> float:
@@ -369,42 +408,216 @@ def time_dfa(lib, steps: int = 50, warmup: int = 10) -> dict:
     }
 
 
-def cpu_baseline(cfg, queries: int) -> dict:
-    """The oracle (CPU restatement of the reference's PyTorch path) on a query subset."""
+def cpu_threads() -> int:
+    """Host cores this process may use: its CPU affinity, bounded by a cgroup
+    CPU quota when one is set (a container's share of a larger host)."""
+    cores = len(os.sched_getaffinity(0))
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if quota != "max":
+            cores = min(cores, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return cores
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+# CPU baseline rows: config -> queries timed (None: all). The oracle's time is
+# proportional to the sampled queries (the value is the full tensor), so a
+# subset's time is scaled by queries / subset to the full workload.
+CPU_ROWS = (("c0", None), ("c1", 2000), ("c2", 1000), ("c3", 8000), ("c4", 500))
+
+
+def cpu_baseline() -> dict:
+    """The oracle (oracle/msda_torch.py, an op-for-op CPU restatement of the
+    reference's PyTorch path) on the host CPU with every available core:
+    c0 forward only at full size; c1-c3 forward + autograd backward in float32
+    and c4 in float32 on value-upcast inputs, each on a query subset scaled to
+    the full query count. Protocol of the survey's CPU plan: warmup 1, then 3
+    repeats of 3 iterations, median of the repeats' per-call seconds."""
     from oracle import msda_torch
 
-    threads = min(16, len(os.sched_getaffinity(0)))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
-    sample = cfg.with_queries(queries)
-    t = make_inputs(sample, device="cpu")
-    value, shapes, loc, attn, grad = (t[k] for k in ("value", "spatial_shapes",
-                                                     "sampling_locations", "attention_weights",
-                                                     "grad_output"))
-    msda_torch.msda_forward_backward(value, shapes, loc, attn, grad)  # warmup
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        msda_torch.msda_forward_backward(value, shapes, loc, attn, grad)
-        times.append(time.perf_counter() - t0)
-    sec = sorted(times)[1]
-    # the query-proportional part dominates; scale the time to the full query count
-    full_sec = sec * cfg.queries / queries
-    fwd_b, bwd_b = algorithmic_bytes(cfg)
+    rows = {}
+    for name, subset in CPU_ROWS:
+        cfg = CONFIGS[name]
+        sample = cfg if subset is None else cfg.with_queries(subset)
+        t = make_inputs(sample, device="cpu")
+        args = [t[k] for k in ("value", "spatial_shapes", "sampling_locations",
+                               "attention_weights")]
+        if cfg.backward:
+            def run():
+                msda_torch.msda_forward_backward(*args, t["grad_output"])
+        else:
+            def run():
+                with torch.no_grad():
+                    msda_torch.msda_forward(*args)
+        run()
+        per_call = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for _ in range(3):
+                run()
+            per_call.append((time.perf_counter() - t0) / 3)
+        sec = statistics.median(per_call) * cfg.queries / sample.queries
+        fwd_b, bwd_b = algorithmic_bytes(cfg)
+        nbytes = fwd_b + (bwd_b if cfg.backward else 0)
+        rows[name] = {
+            "scope": "fwd+bwd" if cfg.backward else "fwd",
+            "ms": round(sec * 1e3, 2),
+            "GBps": round(nbytes / sec / 1e9, 3),
+            "queries_timed": sample.queries,
+            "scale": round(cfg.queries / sample.queries, 3),
+        }
+        print(f"[bench] cpu {name}: {rows[name]}", file=sys.stderr, flush=True)
+    c2 = rows["c2"]
     return {
-        "value": (fwd_b + bwd_b) / full_sec / 1e9,
+        "value": c2["GBps"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
         "sample": (
-            f"oracle/msda_torch.py fwd+autograd bwd, float32, c2 with {queries} of {cfg.queries} "
-            f"queries per camera (all 6 cameras, full value): median of 3 = {sec * 1e3:.1f} ms, "
-            f"scaled x{cfg.queries / queries:g} to {full_sec * 1e3:.0f} ms per full step; "
-            f"{platform.processor() or platform.machine()}"
+            f"oracle/msda_torch.py fwd+autograd bwd, float32, c2 on {c2['queries_timed']} of "
+            f"{CONFIGS['c2'].queries} queries per camera (all 6 cameras, full value), median "
+            f"of 3 repeats x 3 calls scaled x{c2['scale']:g} to {c2['ms']:.0f} ms per full "
+            f"step; {threads} threads on {cpu_model()}"
         ),
+        "cpu_model": cpu_model(),
+        "rows": rows,
     }
 
 
+def time_forward_only(lib, name: str) -> dict:
+    """A forward-only config (c0) through the C-ABI forward, reference protocol."""
+    cfg = CONFIGS[name]
+    t = make_inputs(cfg, device="cuda", with_grad_output=False)
+    out = torch.empty((cfg.batch, cfg.queries, cfg.heads * cfg.channels), device="cuda")
+    args = (t["value"], t["spatial_shapes"], t["level_start_index"], t["sampling_locations"],
+            t["attention_weights"], out, 64)
+    ms = harness_ms(lambda: lib.ms_deform_attn_forward(*args))
+    fwd_b, _ = algorithmic_bytes(cfg)
+    return {"fwd_us": round(ms * 1e3, 2), "effective_GBps": round(fwd_b / (ms * 1e-3) / 1e9, 1)}
+
+
+def time_published_case(lib, dtype) -> dict:
+    """The reference's published case ``bevformer-1l`` in its own timed region
+    (/root/reference/benchmarks/msda/benchmark_msda.py:85-119): allocate the
+    output, one forward launch on the forward input set; allocate the three
+    float32 gradients (torch.empty: these kernels overwrite them, where the
+    reference's accumulate into zero-filled ones), copy the non-contiguous
+    grad_output with ``.contiguous()``, one backward launch on the backward
+    input set (its workspace allocated inside, as the operator's backward
+    does). Every tensor in ``dtype``; warmup 20, 5 repeats x 100, median."""
+    case = make_published_case(dtype=dtype, device="cuda")
+    names = ("value", "spatial_shapes", "level_start_index", "sampling_locations",
+             "attention_weights")
+    fwd = tuple(case["forward_inputs"][k] for k in names)
+    bwd = tuple(case["backward_inputs"][k] for k in names)
+    grad_output = case["backward_inputs"]["grad_output"]
+    assert not grad_output.is_contiguous()
+
+    def launch():
+        out = fwd[0].new_empty((fwd[0].size(0), fwd[3].size(1), fwd[0].size(2) * fwd[0].size(3)))
+        lib.ms_deform_attn_forward(*fwd, out, 64)
+        gv = torch.empty(bwd[0].shape, dtype=torch.float32, device="cuda")
+        gl = torch.empty(bwd[3].shape, dtype=torch.float32, device="cuda")
+        ga = torch.empty(bwd[4].shape, dtype=torch.float32, device="cuda")
+        lib.ms_deform_attn_backward(*bwd, grad_output.contiguous(), gv, gl, ga, 64)
+
+    ms = harness_ms(launch)
+    published = {torch.float32: {"MTT S5000": 4.2387, "A100 (mmcv CUDA)": 4.0895},
+                 torch.bfloat16: {"MTT S5000": 3.9933}}[dtype]
+    return {
+        "fwd_bwd_us": round(ms * 1e3, 1),
+        "published_ms": published,
+        "speedup_vs_S5000": round(published["MTT S5000"] / ms, 2),
+        "note": "reference inputs and timed region; published rows are other hardware "
+                "(benchmarks/msda/README.md:72-73)",
+    }
+
+
+def probe_library():
+    import ctypes
+
+    from muspace_amd.build import PROBE_LIBRARY
+
+    if not PROBE_LIBRARY.is_file():
+        raise SystemExit(f"{PROBE_LIBRARY} is missing; build with `python -m muspace_amd.build`")
+    lib = ctypes.CDLL(str(PROBE_LIBRARY))
+    for fn in (lib.muspace_probe_gather, lib.muspace_probe_atomic):
+        fn.restype = ctypes.c_int
+    lib.muspace_probe_gather.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.muspace_probe_atomic.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+PROBE_MIB = (1, 2, 4, 8, 16)  # footprint per XCD
+
+
+def run_probe(kind: str) -> dict:
+    """Random 128-byte line gathers (16 B a lane, 8 independent loads in
+    flight per lane) or line-wide fp32 atomic adds, every workgroup in its own
+    XCD's region of 1-16 MiB; 2048 workgroups of 256 threads. The atomic sums
+    are checked exactly against the number of adds."""
+    lib = probe_library()
+    blocks, iters = 2048, 512
+    stream = torch.cuda.current_stream().cuda_stream
+    rows = {}
+    max_lines = max(PROBE_MIB) * (1 << 20) // 128
+    buf = torch.zeros(8 * max_lines * 32, device="cuda")
+    sink = torch.empty(blocks * 256, device="cuda")
+    for mib in PROBE_MIB:
+        lines = mib * (1 << 20) // 128
+        if kind == "gather":
+            def launch():
+                rc = lib.muspace_probe_gather(buf.data_ptr(), lines, blocks, iters,
+                                              sink.data_ptr(), stream)
+                assert rc == 0, rc
+            lines_moved = blocks * 256 // 8 * iters
+        else:
+            buf.zero_()
+
+            def launch():
+                rc = lib.muspace_probe_atomic(buf.data_ptr(), lines, blocks, iters, stream)
+                assert rc == 0, rc
+            lines_moved = blocks * 256 // 32 * iters
+        launch()
+        torch.cuda.synchronize()
+        reps = 5
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            launch()
+        end.record()
+        end.synchronize()
+        ms = start.elapsed_time(end) / reps
+        row = {"us": round(ms * 1e3, 1),
+               "G_lines_per_s": round(lines_moved / (ms * 1e-3) / 1e9, 2),
+               "TBps": round(lines_moved * 128 / (ms * 1e-3) / 1e12, 2)}
+        if kind == "atomic":
+            adds = blocks * 256 * iters * (reps + 1)
+            row["sum_exact"] = float(buf.double().sum()) == float(adds)
+        rows[f"{mib}MiB_per_xcd"] = row
+        print(f"[probe] {kind} {mib} MiB/XCD: {row}", file=sys.stderr, flush=True)
+    return {f"{kind}_probe": rows}
+
+
 def read_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (counters cannot be collected
+    inside the timed run itself)."""
     if TRAFFIC_FILE.is_file():
         try:
             return json.loads(TRAFFIC_FILE.read_text()).get("rest_traffic_bytes")
@@ -421,7 +634,14 @@ def main() -> int:
     parser.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extra-configs", action="store_true")
-    parser.add_argument("--cpu-queries", type=int, default=500)
+    parser.add_argument("--repeats", type=int, default=5,
+                        help="the timed steps are split into this many repeats; the median "
+                             "repeat is reported")
+    parser.add_argument("--gather-probe", action="store_true",
+                        help="only the random 128-byte line gather probe (the forward's "
+                             "corner-gather ceiling), then exit")
+    parser.add_argument("--atomic-probe", action="store_true",
+                        help="only the line-wide fp32 atomic-add probe, then exit")
     parser.add_argument("--sca-only", action="store_true",
                         help="only the fused spatial cross-attention scatter-average leg")
     parser.add_argument("--dfa-only", action="store_true",
@@ -455,6 +675,14 @@ def main() -> int:
         print(json.dumps({"copy_probe_bytes": n * 4, "launches": 5}))
         return 0
 
+    if args.gather_probe or args.atomic_probe:
+        out = {}
+        for kind, wanted in (("gather", args.gather_probe), ("atomic", args.atomic_probe)):
+            if wanted:
+                out.update(run_probe(kind))
+        print(json.dumps(out))
+        return 0
+
     from muspace_amd.runtime.native import load_native_module
 
     lib = load_native_module()
@@ -472,7 +700,7 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     print(f"[bench] inputs for {cfg.name}", file=sys.stderr, flush=True)
     step = Step(lib, cfg, torch.float32, torch.float32, dev, serial=args.serial_backward)
-    res = time_steps(step, args.steps, args.warmup)
+    res = time_steps(step, args.steps, args.warmup, repeats=args.repeats)
     fwd_b, bwd_b = algorithmic_bytes(cfg)
     gbps = (fwd_b + bwd_b) / (res["ms_per_step"] * 1e-3) / 1e9
     print(f"[bench] {cfg.name}: {res}", file=sys.stderr, flush=True)
@@ -499,7 +727,14 @@ def main() -> int:
             }
             del s
             torch.cuda.empty_cache()
-        extra["bevformer-1l-published_ms"] = {"MTT S5000": 4.2387, "A100 (mmcv CUDA)": 4.0895}
+        print("[bench] extra c0 forward", file=sys.stderr, flush=True)
+        extra["c0-float32-forward"] = time_forward_only(lib, "c0")
+        torch.cuda.empty_cache()
+        for dtype in (torch.float32, torch.bfloat16):
+            label = str(dtype).replace("torch.", "")
+            print(f"[bench] extra published bevformer-1l {label}", file=sys.stderr, flush=True)
+            extra[f"bevformer-1l-published-case-{label}"] = time_published_case(lib, dtype)
+            torch.cuda.empty_cache()
         print("[bench] extra sca-scatter-div", file=sys.stderr, flush=True)
         extra["sca-scatter-div-float32"] = time_sca(lib)
         torch.cuda.empty_cache()
@@ -513,7 +748,9 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(cfg, args.cpu_queries)
+        cpu = cpu_baseline()
+        if "c0-float32-forward" in extra:
+            extra["c0-float32-forward"]["cpu_fwd_us"] = round(cpu["rows"]["c0"]["ms"] * 1e3, 1)
 
     rest_b = backward_rest_bytes(cfg)
     rest_achieved = rest_b / (res["rest_ms"] * 1e-3) / 1e9
@@ -525,6 +762,9 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(res["ms_per_step"], 4),
+        "timing": {"repeats": len(res["repeat_ms_per_step"]), "statistic": "median of repeats",
+                   "repeat_ms_per_step": res["repeat_ms_per_step"],
+                   "mean_ms_per_step": round(res["mean_ms_per_step"], 4)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -553,6 +793,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(rest_achieved / HBM_PEAK_GBPS, 4),
             "traffic": read_traffic(),
+            "traffic_source": str(TRAFFIC_FILE.relative_to(ROOT)),
         },
         "cpu_baseline": cpu,
         "other_configs": extra,

@@ -28,6 +28,10 @@ DEPENDS = (
     REPO_DIR / "include" / "muspace_dfa.h",
 )
 LIBRARY = PACKAGE_DIR / "native" / "libmuspace_msda.so"
+# memory-system probes for bench.py (--gather-probe, --atomic-probe); not
+# loaded by the operators
+PROBE_SOURCES = (PACKAGE_DIR / "csrc" / "probes.hip",)
+PROBE_LIBRARY = PACKAGE_DIR / "native" / "libmuspace_probes.so"
 OFFLOAD_ARCH = "gfx950"
 
 # -packed-fp32-ops keeps the compiler from emitting packed fp32 VALU
@@ -58,25 +62,31 @@ def hipcc() -> str:
     raise FileNotFoundError("hipcc not found; ROCm is required to build libmuspace_msda.so")
 
 
-def build_command(output: Path) -> list[str]:
-    return [hipcc(), *HIPCC_FLAGS, *(str(s) for s in SOURCES), "-o", str(output)]
+def build_command(output: Path, sources=SOURCES) -> list[str]:
+    return [hipcc(), *HIPCC_FLAGS, *(str(s) for s in sources), "-o", str(output)]
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile the library (always) and move it into place atomically."""
-    LIBRARY.parent.mkdir(parents=True, exist_ok=True)
-    tmp = LIBRARY.with_name(LIBRARY.name + f".tmp{os.getpid()}")
-    cmd = build_command(tmp)
+def _compile(library: Path, sources, verbose: bool) -> Path:
+    library.parent.mkdir(parents=True, exist_ok=True)
+    tmp = library.with_name(library.name + f".tmp{os.getpid()}")
+    cmd = build_command(tmp, sources)
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         tmp.unlink(missing_ok=True)
         raise RuntimeError(
-            f"hipcc failed ({proc.returncode}) building {LIBRARY.name}:\n{proc.stderr[-4000:]}"
+            f"hipcc failed ({proc.returncode}) building {library.name}:\n{proc.stderr[-4000:]}"
         )
-    os.replace(tmp, LIBRARY)
-    return LIBRARY
+    os.replace(tmp, library)
+    return library
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the MSDA library and the probe library (always), each moved
+    into place atomically; returns the MSDA library's path."""
+    _compile(PROBE_LIBRARY, PROBE_SOURCES, verbose)
+    return _compile(LIBRARY, SOURCES, verbose)
 
 
 def main(argv: list[str] | None = None) -> int:

@@ -175,6 +175,48 @@ def backward_rest_bytes(cfg: MSDAConfig, value_dtype: torch.dtype = torch.float3
     return n_value * vb + n_out * vb + 4 * (n_value + 2 * n_attn + n_attn)
 
 
+# ------------------------------------------- the reference's published case ---
+
+
+def make_published_case(
+    *,
+    seed: int = DEFAULT_SEED,
+    dtype: torch.dtype = torch.float32,
+    device: str | torch.device = "cpu",
+) -> dict[str, dict[str, torch.Tensor]]:
+    """The reference's published MSDA case ``bevformer-1l``, as its benchmark
+    draws it (/root/reference/benchmarks/msda/msda_single_level_case.py:41-82):
+    separate forward and backward input sets from generators seeded ``seed``
+    and ``seed + 1`` (value scale 1.38 and 1.25), one 200x200 level, 40000
+    queries of 8 heads x 32 channels and 4 points, locations
+    ``U(0, 1) * 1.035 - 0.0175``, attention weights 0.25, every tensor in
+    ``dtype`` (geometry included), and a non-contiguous grad_output: a
+    ``[40000, 256, 2]`` draw scaled by 6.3e-6 and permuted to
+    ``[2, 40000, 256]`` (strides (1, 512, 2)), so the timed region keeps the
+    reference's ``grad_output.contiguous()`` copy."""
+    batch, queries, heads, channels, points = 2, 40000, 8, 32, 4
+
+    def draw(gen, scale):
+        value = torch.randn((batch, 40000, heads, channels), generator=gen) * scale
+        loc = torch.rand((batch, queries, heads, 1, points, 2), generator=gen) * 1.035 - 0.0175
+        return {
+            "value": value.to(dtype).to(device),
+            "spatial_shapes": torch.tensor([[200, 200]], dtype=torch.int64).to(device),
+            "level_start_index": torch.tensor([0], dtype=torch.int64).to(device),
+            "sampling_locations": loc.to(dtype).to(device),
+            "attention_weights": torch.full((batch, queries, heads, 1, points), 0.25,
+                                            dtype=dtype).to(device),
+        }
+
+    forward_gen = torch.Generator(device="cpu").manual_seed(seed)
+    backward_gen = torch.Generator(device="cpu").manual_seed(seed + 1)
+    forward_inputs = draw(forward_gen, 1.38)
+    backward_inputs = draw(backward_gen, 1.25)
+    grad = torch.randn((queries, heads * channels, batch), generator=backward_gen) * 6.3e-6
+    backward_inputs["grad_output"] = grad.to(dtype).to(device).permute(2, 0, 1)
+    return {"forward_inputs": forward_inputs, "backward_inputs": backward_inputs}
+
+
 # ------------------------------------------------ spatial cross-attention ---
 
 SCA_BEV = (200, 200)  # BEVFormer-base BEV grid: 40000 queries

@@ -269,3 +269,30 @@ def test_sparsedrive_missing_ops_module_is_a_patch_error(monkeypatch):
     monkeypatch.setitem(sys.modules, "projects.mmdet3d_plugin.ops", None)
     with pytest.raises(PatchError, match="SparseDrive ops package import failed"):
         SparseDrivePatcher().apply()
+
+
+def test_two_patchers_share_one_extension_guard(monkeypatch):
+    """The guard belongs to the patcher that installed it: a second patcher
+    neither stacks another guard nor removes the first one's."""
+    _install_fake_module(monkeypatch, TARGET)
+    ext_loader, original_load_ext = _install_fake_ext_loader(monkeypatch)
+    first, second = DefaultPatcher(), DefaultPatcher()
+    first.apply()
+    guarded = ext_loader.load_ext
+    second.apply()
+    assert ext_loader.load_ext is guarded
+    second.restore()
+    assert ext_loader.load_ext is guarded
+    first.restore()
+    assert ext_loader.load_ext is original_load_ext
+    assert not hasattr(ext_loader, "_muspace_original_load_ext")
+
+
+def test_strict_then_compat_restores_the_original(monkeypatch):
+    module, original = _install_fake_module(monkeypatch, TARGET)
+    patcher = DefaultPatcher()
+    assert patcher.apply(strict=True).action == "applied"
+    assert patcher.apply(strict=False).action == "applied"
+    assert getattr(module, ATTR).__name__ == "muspace_multi_scale_deformable_attn_compat"
+    assert patcher.restore().patched_modules == (TARGET,)
+    assert getattr(module, ATTR) is original
