@@ -237,11 +237,21 @@ struct CameraSlots {
 // lane i < NG*NS computes one sample's bilinear tap -- the four corner byte
 // offsets (kOobOffset for a corner outside the level) and the four weights
 // with the attention weight folded in -- into a wavefront-private LDS table;
-// then lane group g gathers the corner rows of its NS samples with 16-byte
-// buffer loads (out-of-range offsets read zeros) and accumulates. The next
-// step's geometry is loaded before the gathers are waited for (vmcnt counts
-// in issue order), and every load is unconditional (clamped indices): a load
-// inside a branch is waited for before the branch joins.
+// lane group g then gathers the corner rows of its NS samples with 16-byte
+// buffer loads (out-of-range offsets read zeros) and accumulates.
+//
+// Software pipeline (NS >= 4): a step's gathers are issued in two halves and
+// the loop always keeps one half in flight while it consumes the other --
+// issue H1(st), consume H0(st), tap of step st+1, issue H0(st+1), consume
+// H1(st) -- so a wavefront never waits for all of a step's corner rows with
+// nothing else outstanding (with two wavefronts per SIMD that wait left the
+// memory pipe idle: c2 forward 382 -> 366 us). NS <= 2 issues and consumes
+// a step in place. The next step's
+// geometry is loaded right after its first stage is issued (vmcnt counts in
+// issue order), and every load is unconditional (clamped indices; a load
+// inside a branch is waited for before the branch joins). The tap tables are
+// double-buffered by step parity and padded by one entry per lane group, so
+// the NG groups' reads of one sample slot fall in different LDS banks.
 // value_bytes < 2^31 (checked on the host) keeps every offset in 32 bits.
 //
 // kSoftmax: `attn` holds logits, and each unit's weights are their softmax
@@ -264,14 +274,25 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   constexpr int VB = static_cast<int>(sizeof(VT));
   constexpr int KQ = C / CPL;
   constexpr int NG = kWave / KQ;
+  // stages per step: NS >= 4 gathers a step in two halves; NS <= 2 in one
+  constexpr int NSPLIT = NS >= 4 ? 2 : 1;
+  constexpr int NH = NS / NSPLIT;  // samples per stage
+  // tap table: one padding entry per lane group when NS >= 4, so the groups'
+  // reads of one sample slot fall in different LDS banks (NS = 1 is
+  // conflict-free as it is; NS = 2 measured no gain)
+  constexpr int PAD = NSPLIT == 2 ? 1 : 0;
+  static_assert(NSPLIT == 1 || NS % 2 == 0, "two equal halves");
+  constexpr int TW = kWave + PAD * (kWave / NS);  // table entries per wavefront
   static_assert(C % CPL == 0 && (KQ & (KQ - 1)) == 0 && KQ <= kWave, "bad row layout");
   static_assert(NG * NS <= kWave, "one tap per lane");
 
   __shared__ Level lv[kMaxLevels];
-  __shared__ u32x4 tap_off[kBlock];
-  __shared__ float4 tap_w[kBlock];
-  // kSoftmax, per unit slot: the current step's rescale and 1/sum
-  __shared__ float2 unit_norm[kSoftmax ? kBlock : 1];
+  // double-buffered by step parity when a step's tap is written while the
+  // previous step is still being consumed (NSPLIT == 2)
+  __shared__ u32x4 tap_off[NSPLIT][(kBlock / kWave) * TW];
+  __shared__ float4 tap_w[NSPLIT][(kBlock / kWave) * TW];
+  // kSoftmax, per step parity and unit slot: the step's rescale and 1/sum
+  __shared__ float2 unit_norm[2][kSoftmax ? kBlock : 1];
   stage_levels(lv, shapes, starts, s);
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(value, value_bytes);
 
@@ -286,8 +307,9 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   // the sample this lane computes the tap of: sample tj of lane group tg
   const int tg = min(lane / NS, NG - 1), tj = lane % NS;
   const int tgi = tg & (GU - 1), tslot = tg >> plan.gu_log2;
-  u32x4 *my_off = tap_off + wave * kWave;
-  float4 *my_w = tap_w + wave * kWave;
+  // table entry of lane group g's sample j: g * (NS + PAD) + j
+  const int my_entry = wave * TW + tg * (NS + PAD) + tj;
+  const int grp_entry = wave * TW + grp * (NS + PAD);
 
   const int64_t wave_id = static_cast<int64_t>(lb) * (kBlock / kWave) + wave;
   const int chunks = (s.lp + GU * NS - 1) / (GU * NS);
@@ -330,7 +352,7 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
     m_run = m_new;
     if (lane < NG * NS && (lane & (tb - 1)) == 0) {
       // hardware reciprocal (1 ulp); 1/0 = inf keeps an all -inf unit NaN
-      unit_norm[wave * kWave + tslot] = make_float2(sc, __builtin_amdgcn_rcpf(s_run));
+      unit_norm[st & 1][wave * kWave + tslot] = make_float2(sc, __builtin_amdgcn_rcpf(s_run));
     }
   };
   auto load_geometry = [&](int st) {
@@ -350,57 +372,51 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
     a = load_nt(&attn[o]);
     unit_base = static_cast<uint32_t>((slab * MC + tu.m * C) * VB);
   };
-  load_geometry(0);
-  float acc[CPL];
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
-
-  for (int st = 0; st < steps; ++st) {
-    if (st % chunks == 0) out.fetch_count(tk_cur, ou.b, s);
-    // A. this lane's tap into the wavefront's table
-    {
-      const Level L = lv[level_of_sample(sm, s)];
-      const Tap t = make_tap(lx, ly, L, ok);
-      float ai = ok ? a : 0.0f;
-      if constexpr (kSoftmax) {
-        softmax_step(st);
-        ai = e_cur;  // 0 unless ok
-      }
-      const uint32_t row = static_cast<uint32_t>(MC * VB);
-      const uint32_t c00 = unit_base + static_cast<uint32_t>(L.start + t.cell00) * row;
-      const uint32_t c10 = c00 + static_cast<uint32_t>(L.w) * row;
-      u32x4 off;
-      off.x = t.y0ok && t.x0ok ? c00 : kOobOffset;
-      off.y = t.y0ok && t.x1ok ? c00 + row : kOobOffset;
-      off.z = t.y1ok && t.x0ok ? c10 : kOobOffset;
-      off.w = t.y1ok && t.x1ok ? c10 + row : kOobOffset;
-      my_off[lane] = off;
-      my_w[lane] = make_float4(ai * (t.wy0 * t.wx0), ai * (t.wy0 * t.wx1), ai * (t.wy1 * t.wx0),
-                               ai * (t.wy1 * t.wx1));
+  // A. this lane's tap of step st (geometry loaded) into table st & 1
+  auto tap = [&](int st) {
+    const Level L = lv[level_of_sample(sm, s)];
+    const Tap t = make_tap(lx, ly, L, ok);
+    float ai = ok ? a : 0.0f;
+    if constexpr (kSoftmax) {
+      softmax_step(st);
+      ai = e_cur;  // 0 unless ok
     }
-    // B. gathers of this lane group's NS samples, then the next step's geometry
-    u32x4 raw[NS][4];
+    const uint32_t row = static_cast<uint32_t>(MC * VB);
+    const uint32_t c00 = unit_base + static_cast<uint32_t>(L.start + t.cell00) * row;
+    const uint32_t c10 = c00 + static_cast<uint32_t>(L.w) * row;
+    u32x4 off;
+    off.x = t.y0ok && t.x0ok ? c00 : kOobOffset;
+    off.y = t.y0ok && t.x1ok ? c00 + row : kOobOffset;
+    off.z = t.y1ok && t.x0ok ? c10 : kOobOffset;
+    off.w = t.y1ok && t.x1ok ? c10 + row : kOobOffset;
+    if (lane < NG * NS) {  // lanes past the taps would alias group NG-1's entries
+      const int tb = st & (NSPLIT - 1);
+      tap_off[tb][my_entry] = off;
+      tap_w[tb][my_entry] = make_float4(ai * (t.wy0 * t.wx0), ai * (t.wy0 * t.wx1),
+                                        ai * (t.wy1 * t.wx0), ai * (t.wy1 * t.wx1));
+    }
+  };
+  // B. gathers of stage h of step st (this lane group's samples h*NH ..
+  // h*NH + NH - 1)
+  const uint32_t ch = static_cast<uint32_t>(k * 16);
+  auto issue = [&](int st, int h, u32x4 (&raw)[NH][4]) {
 #pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      const u32x4 off = my_off[grp * NS + j];
-      const uint32_t ch = static_cast<uint32_t>(k * 16);
+    for (int j = 0; j < NH; ++j) {
+      const u32x4 off = tap_off[st & (NSPLIT - 1)][grp_entry + h * NH + j];
       raw[j][0] = buffer_load16(vr, off.x + ch);
       raw[j][1] = buffer_load16(vr, off.y + ch);
       raw[j][2] = buffer_load16(vr, off.z + ch);
       raw[j][3] = buffer_load16(vr, off.w + ch);
     }
-    load_geometry(st + 1);
-    // C. accumulate
-    if constexpr (kSoftmax) {
-      if (chunks > 1) {
-        const float sc = unit_norm[wave * kWave + slot].x;
+  };
+  // C. accumulate half h of step st
+  float acc[CPL];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) acc[j] *= sc;
-      }
-    }
+  for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
+  auto consume = [&](int st, int h, const u32x4 (&raw)[NH][4]) {
 #pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      const float4 w = my_w[grp * NS + j];
+    for (int j = 0; j < NH; ++j) {
+      const float4 w = tap_w[st & (NSPLIT - 1)][grp_entry + h * NH + j];
       float v0[CPL], v1[CPL], v2[CPL], v3[CPL];
       decode16(VT(), raw[j][0], v0);
       decode16(VT(), raw[j][1], v1);
@@ -411,31 +427,80 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
         acc[c] += w.x * v0[c] + w.y * v1[c] + w.z * v2[c] + w.w * v3[c];
       }
     }
-    // D. end of the unit: sum the GU groups (lane distance KQ, 2KQ, ...), store
-    if (st % chunks == chunks - 1) {
-      for (int off = KQ; off < KQ * GU; off <<= 1) {
+  };
+
+  // the start of step st: its unit's epilogue data; kSoftmax with a unit of
+  // several steps: rescale to the step's running max
+  auto begin_step = [&](int st) {
+    if (st % chunks == 0) out.fetch_count(tk_cur, ou.b, s);
+    if constexpr (kSoftmax) {
+      if (chunks > 1) {
+        const float sc = unit_norm[st & 1][wave * kWave + slot].x;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) acc[j] += __shfl_xor(acc[j], off, kWave);
+        for (int j = 0; j < CPL; ++j) acc[j] *= sc;
       }
-      if constexpr (kSoftmax) {
-        const float inv = unit_norm[wave * kWave + slot].y;
+    }
+  };
+  // D. the end of step st; at the end of a unit sum the GU groups (lane
+  // distance KQ, 2KQ, ...) and store. Steps past the last one (the step
+  // pipeline rounds up to pairs) end nothing.
+  auto end_step = [&](int st) {
+    if (st >= steps || st % chunks != chunks - 1) return;
+    for (int off = KQ; off < KQ * GU; off <<= 1) {
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) acc[j] *= inv;
-      }
-      const int64_t u64 = u_first + static_cast<int64_t>(st / chunks) * UW + slot;
-      if (u64 < s.units && gi == 0) {
-        out.template put<C, CPL>(ou.b, ou.q, ou.m, k, acc, tk_cur, s);
-      }
-      if constexpr (Out::kLoadsAhead) {
-        ou = on;
-        tk_cur = tk_next;
-        on.advance(UW, s);
-        out.fetch_index(tk_next, on.q);
-      } else {
-        ou.advance(UW, s);
-      }
+      for (int j = 0; j < CPL; ++j) acc[j] += __shfl_xor(acc[j], off, kWave);
+    }
+    if constexpr (kSoftmax) {
+      const float inv = unit_norm[st & 1][wave * kWave + slot].y;
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
+      for (int j = 0; j < CPL; ++j) acc[j] *= inv;
+    }
+    const int64_t u64 = u_first + static_cast<int64_t>(st / chunks) * UW + slot;
+    if (u64 < s.units && gi == 0) {
+      out.template put<C, CPL>(ou.b, ou.q, ou.m, k, acc, tk_cur, s);
+    }
+    if constexpr (Out::kLoadsAhead) {
+      ou = on;
+      tk_cur = tk_next;
+      on.advance(UW, s);
+      out.fetch_index(tk_next, on.q);
+    } else {
+      ou.advance(UW, s);
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) acc[j] = 0.0f;
+  };
+  // Past the last step the taps have zero weights and out-of-range offsets
+  // (which read zeros), so the pipeline's look-ahead is harmless.
+  u32x4 raw0[NH][4], raw1[NH][4];
+  load_geometry(0);
+  if constexpr (NSPLIT == 2) {
+    tap(0);
+    issue(0, 0, raw0);
+    load_geometry(1);
+    for (int st = 0; st < steps; ++st) {
+      begin_step(st);
+      issue(st, 1, raw1);
+      consume(st, 0, raw0);
+      // the next step's tap and first half, then its successor's geometry
+      tap(st + 1);
+      issue(st + 1, 0, raw0);
+      load_geometry(st + 2);
+      consume(st, 1, raw1);
+      end_step(st);
+    }
+  } else {
+    // one or two samples per group: a step's few gathers are issued and
+    // consumed in place (double-buffering whole steps measured slower here:
+    // c1 179 -> 201 us, c3 133 -> 137 us)
+    (void)raw1;
+    for (int st = 0; st < steps; ++st) {
+      begin_step(st);
+      tap(st);
+      issue(st, 0, raw0);
+      load_geometry(st + 1);
+      consume(st, 0, raw0);
+      end_step(st);
     }
   }
 }
