@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define MUSPACE_MSDA_ABI_VERSION 3
+#define MUSPACE_MSDA_ABI_VERSION 4
 
 /* the library is built with -fvisibility=hidden; only these symbols export */
 #if defined(__GNUC__)
@@ -97,6 +97,27 @@ MUSPACE_API int ms_deform_attn_backward(const void *value, int value_dtype, cons
                             int64_t batch, int64_t spatial_size, int64_t num_heads,
                             int64_t channels, int64_t num_levels, int64_t num_query,
                             int64_t num_point, int64_t im2col_step, void *stream);
+
+/* ms_deform_attn_backward that allocates nothing: no hipMalloc, hipFree or
+ * allocating library call, for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid it). No reference
+ * counterpart. Same arguments and results as ms_deform_attn_backward. Its
+ * scratch is one file-scope device array of MUSPACE_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends; the batch is processed in passes of as
+ * many batch entries as fit it (each pass is exact: a batch entry's gradients
+ * depend on that entry alone). A shape whose single batch entry needs more
+ * scratch than that is rejected with MUSPACE_ERANGE before anything runs.
+ * Every call on one GPU uses that GPU's array, so calls that overlap on one
+ * GPU (concurrent streams, or threads without stream ordering) race; calls
+ * ordered on one stream are safe. */
+#define MUSPACE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+MUSPACE_API int ms_deform_attn_backward_noalloc(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_weights, int geometry_dtype, const void *grad_output,
+    float *grad_value, float *grad_sampling_locations, float *grad_attention_weights,
+    int64_t batch, int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *stream);
 
 /* Scratch bytes ms_deform_attn_backward_ws needs for these dims (0: the shape
  * takes the atomic fallback and needs none). No reference counterpart: the

@@ -12,6 +12,7 @@
 #include <climits>
 #include <cstdint>
 #include <initializer_list>
+#include <mutex>
 #include <type_traits>
 #include <cstdarg>
 #include <cstdio>
@@ -835,6 +836,61 @@ size_t softmax_workspace_bytes(const msda::Shape &s, int value_dtype, int geomet
   return probs_bytes(s, geometry_dtype) + tiles;
 }
 
+// Scratch of ms_deform_attn_backward_noalloc: one array per GPU, in the code
+// object's zero-initialised data, held until the process ends. In host code
+// `scratch` is a host-side stand-in for the symbol; the device address comes
+// from hipGetSymbolAddress, once per device.
+constexpr size_t kNoAllocScratchBytes = MUSPACE_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` into *out.
+int scratch_on_current_device(const char *fn, void **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return fail(MUSPACE_EINVAL, "%s: no current HIP device (or device index >= %d)", fn,
+                kMaxDevices);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return fail(MUSPACE_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                  fn, dev, hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ok();
+}
+
+// Batch entries per pass of the no-allocation backward: the largest count
+// whose tile workspace fits the scratch (0 if one entry does not fit).
+int64_t noalloc_batch_step(const msda::Shape &s, int value_dtype, size_t *one_entry_bytes) {
+  int64_t nb = s.batch;
+  *one_entry_bytes = 0;
+  while (nb >= 1) {
+    msda::Shape sc = s;
+    sc.batch = static_cast<int>(nb);
+    sc.units = static_cast<int>(nb * s.queries * s.heads);
+    TileWorkspace w;
+    if (!plan_tile_workspace(sc, value_dtype, w)) return 0;
+    if (nb == 1) *one_entry_bytes = w.bytes;
+    if (w.bytes <= kNoAllocScratchBytes) return nb;
+    // the workspace grows about linearly with the batch entries
+    const int64_t scaled = static_cast<int64_t>(
+        static_cast<double>(nb) * static_cast<double>(kNoAllocScratchBytes) /
+        static_cast<double>(w.bytes));
+    nb = scaled < nb ? scaled : nb - 1;
+  }
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1144,6 +1200,68 @@ int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *s
                                workspace, bytes, st);
   if (workspace) (void)hipFreeAsync(workspace, st);
   return rc;
+}
+
+int ms_deform_attn_backward_noalloc(const void *value, int value_dtype,
+                                    const int64_t *spatial_shapes,
+                                    const int64_t *level_start_index,
+                                    const void *sampling_locations,
+                                    const void *attention_weights, int geometry_dtype,
+                                    const void *grad_output, float *grad_value,
+                                    float *grad_sampling_locations,
+                                    float *grad_attention_weights, int64_t batch,
+                                    int64_t spatial_size, int64_t num_heads, int64_t channels,
+                                    int64_t num_levels, int64_t num_query, int64_t num_point,
+                                    int64_t im2col_step, void *stream) {
+  static const char *fn = "ms_deform_attn_backward_noalloc";
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  msda::Shape s;
+  if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
+  TileWorkspace w;
+  const bool tiles = needs_data(s) && s.lp > 0 && plan_tile_workspace(s, value_dtype, w);
+  if (!tiles) {  // zero gradients or the atomic fallback: no scratch at all
+    return backward_impl(fn, value, value_dtype, spatial_shapes, level_start_index,
+                         sampling_locations, attention_weights, geometry_dtype, grad_output,
+                         grad_value, grad_sampling_locations, grad_attention_weights, a, nullptr,
+                         0, st);
+  }
+  if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+      !attention_weights || !grad_output || !grad_value || !grad_sampling_locations ||
+      !grad_attention_weights) {
+    return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+  }
+  size_t one_entry = 0;
+  const int64_t step = noalloc_batch_step(s, value_dtype, &one_entry);
+  if (step <= 0) {
+    return fail(MUSPACE_ERANGE,
+                "%s: one batch entry of this shape needs %zu bytes of scratch; the "
+                "no-allocation scratch holds %zu (use ms_deform_attn_backward or _ws)",
+                fn, one_entry, kNoAllocScratchBytes);
+  }
+  void *ws = nullptr;
+  if (int rc = scratch_on_current_device(fn, &ws)) return rc;
+  const size_t vb = value_dtype == MUSPACE_DTYPE_F32 ? 4 : 2;
+  const size_t gb = geometry_dtype == MUSPACE_DTYPE_F32 ? 4 : 2;
+  const size_t per_value = static_cast<size_t>(spatial_size) * num_heads * channels;
+  const size_t per_sample = static_cast<size_t>(num_query) * num_heads * num_levels * num_point;
+  const size_t per_out = static_cast<size_t>(num_query) * num_heads * channels;
+  for (int64_t b0 = 0; b0 < batch; b0 += step) {
+    const int64_t nb = batch - b0 < step ? batch - b0 : step;
+    const Args ab{nb, spatial_size, num_heads, channels, num_levels, num_query, num_point, nb};
+    const size_t b = static_cast<size_t>(b0);
+    const int rc = backward_impl(
+        fn, static_cast<const unsigned char *>(value) + b * per_value * vb, value_dtype,
+        spatial_shapes, level_start_index,
+        static_cast<const unsigned char *>(sampling_locations) + b * per_sample * 2 * gb,
+        static_cast<const unsigned char *>(attention_weights) + b * per_sample * gb,
+        geometry_dtype, static_cast<const unsigned char *>(grad_output) + b * per_out * vb,
+        grad_value + b * per_value, grad_sampling_locations + b * per_sample * 2,
+        grad_attention_weights + b * per_sample, ab, ws, kNoAllocScratchBytes, st);
+    if (rc != MUSPACE_OK) return rc;
+  }
+  return ok();
 }
 
 int ms_deform_attn_forward_softmax(const void *value, int value_dtype,

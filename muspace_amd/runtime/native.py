@@ -25,7 +25,7 @@ from pathlib import Path
 from typing import Any, Callable
 
 LIBRARY_RELPATH = "native/libmuspace_msda.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
@@ -55,6 +55,12 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
         + [_c_int64] * 8
         + [_c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "ms_deform_attn_backward_noalloc": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr],
     ),
     "ms_deform_attn_backward_workspace_size": (ctypes.c_size_t, [_c_int] + [_c_int64] * 7),
     "ms_deform_attn_backward_bin": (
@@ -192,6 +198,7 @@ class NativeLibrary:
             "check_backward": self.check_backward,
             "ms_deform_attn_forward": self.ms_deform_attn_forward,
             "ms_deform_attn_backward": self.ms_deform_attn_backward,
+            "ms_deform_attn_backward_noalloc": self.ms_deform_attn_backward_noalloc,
             "backward_workspace": self.backward_workspace,
             "ms_deform_attn_backward_bin": self.ms_deform_attn_backward_bin,
             "ms_deform_attn_backward_rest": self.ms_deform_attn_backward_rest,
@@ -363,6 +370,31 @@ class NativeLibrary:
                                 grad_output, grad_value, grad_sampling_locations,
                                 grad_attention_weights, im2col_step, workspace,
                                 self._stream(value))
+
+    def ms_deform_attn_backward_noalloc(
+        self, value, spatial_shapes, level_start_index, sampling_locations,
+        attention_weights, grad_output, grad_value, grad_sampling_locations,
+        grad_attention_weights, im2col_step: int,
+    ) -> None:
+        """:meth:`ms_deform_attn_backward` through the C entry that allocates
+        nothing: its scratch is the library's fixed per-GPU array
+        (MUSPACE_NOALLOC_SCRATCH_BYTES), the batch processed in passes that fit
+        it. Calls that overlap on one GPU race on that array."""
+        import torch
+
+        dims = self.check_backward(value, spatial_shapes, level_start_index, sampling_locations,
+                                   attention_weights, grad_output, grad_value,
+                                   grad_sampling_locations, grad_attention_weights)
+        with torch.cuda.device(value.device):
+            rc = self._raw["ms_deform_attn_backward_noalloc"](
+                value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
+                level_start_index.data_ptr(), sampling_locations.data_ptr(),
+                attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
+                grad_output.data_ptr(), grad_value.data_ptr(),
+                grad_sampling_locations.data_ptr(), grad_attention_weights.data_ptr(),
+                *dims, int(im2col_step), self._stream(value),
+            )
+        self._raise_on(rc, "ms_deform_attn_backward_noalloc")
 
     def ms_deform_attn_backward_softmax(
         self, value, spatial_shapes, level_start_index, sampling_locations,

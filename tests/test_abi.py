@@ -94,6 +94,19 @@ def test_backward_validation_fails_before_any_launch(native_lib):
     assert "null tensor pointer" in native_lib.last_error()
 
 
+def test_noalloc_backward_rejects_an_entry_larger_than_its_scratch(native_lib):
+    """One batch entry of 8 heads x 100000 queries x 32 samples needs about
+    420 MB of tile scratch, more than the 64 MiB array: MUSPACE_ERANGE before
+    anything runs (the pointers are stand-ins; nothing may read them)."""
+    fn = native_lib.raw("ms_deform_attn_backward_noalloc")
+    args = [1, 0, 1, 1, 1, 1, 0, 1, 1, 1, 1,
+            2, 30825, 8, 32, 4, 100000, 8, 64, None]
+    assert fn(*args) == 2  # MUSPACE_ERANGE
+    assert "needs" in native_lib.last_error() and "scratch" in native_lib.last_error()
+    args[1:2] = [9]  # a bad dtype is still MUSPACE_EINVAL, first
+    assert fn(*args) == 1
+
+
 def _backward_ws_args(**overrides):
     args = dict(value=1, value_dtype=0, shapes=1, starts=1, loc=1, attn=1, geometry_dtype=0,
                 grad=1, grad_value=1, grad_loc=1, grad_attn=1, batch=2, spatial=4, heads=1,
