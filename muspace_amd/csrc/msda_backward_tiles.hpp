@@ -634,9 +634,11 @@ __device__ __forceinline__ void store_corner_dots(const float (&dd)[4], int k, f
 // Memory order: gfx950 counts loads and stores in one in-order vmcnt, so a
 // wait for one load also waits for everything issued before it. The next
 // batch's records are loaded first thing in a batch (into registers); the
-// next item's value tile is copied into LDS by buffer-to-LDS loads issued at
-// the end of the previous batch (no registers held), waited for before the
-// owner phase; the owner loop keeps NR grad_out rows in flight per group.
+// next item's value tile is loaded into registers at the end of phase E of
+// the previous batch and written to LDS in phase C; the owner loop keeps NR
+// grad_out rows in flight per group. No buffer-to-LDS loads: after one, the
+// compiler makes every LDS access wait for it (and so for all earlier loads
+// and stores).
 template <typename VT, int C>
 __global__ void __launch_bounds__(kTileBlock)
     msda_tile_backward(const VT *__restrict__ value, uint32_t value_bytes,
@@ -765,35 +767,43 @@ __global__ void __launch_bounds__(kTileBlock)
   auto slab_offset = [&](const Item &d) {
     return static_cast<size_t>(d.b) * s.spatial * MC + d.m * C;
   };
-  // Value tile (cells [0, T]^2 of the item's frame) of d into LDS with
-  // buffer-to-LDS loads: 16-byte unit u of the tile goes to vt + 16 u; each
-  // wavefront moves 64 consecutive units (lane i to M0 + 16 i), so the LDS
-  // base of a load is wavefront-uniform. Units of cells outside the level use
-  // an offset past the end of value and read zeros. value_bytes < 2^31 is
-  // checked on the host.
-  auto stage_value_tile = [&](const Item &d) {
+  // Value tile (cells [0, T]^2 of the item's frame) of d: 16-byte unit u =
+  // tid + v * kTileBlock of the tile goes to vt + 16 u. The next item's tile
+  // is loaded into registers at the end of phase E of the batch before its
+  // first one and written to LDS in that first batch's phase C (vt is read
+  // only in phase D). Every load is issued (an out-of-range offset, which
+  // reads zeros, for units past the tile, cells outside the level and
+  // batches that start no item). Buffer-to-LDS loads held no registers, but
+  // every LDS access after one waits for it -- and, vmcnt counting in issue
+  // order, for every store issued before it -- so each batch's first LDS
+  // access waited for the previous batch's scattered gradient stores to
+  // drain. value_bytes < 2^31 is checked on the host.
+  uint4 vt_next[VPT];
+  auto load_value_tile = [&](const Item &d, bool want) {
     const TileGeom g = item_geom(d);
     const Level L = lv[g.l];
     const size_t slab = slab_offset(d);
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
       const int unit = tid + v * kTileBlock;
-      if (unit < NPOS * UPV) {
-        const int cell = unit / UPV, kk = unit % UPV;
-        const int y = g.y_lo + cell / TV, x = g.x_lo + cell % TV;
-        const uint32_t off =
-            y < L.h && x < L.w
-                ? static_cast<uint32_t>(
-                      (slab + static_cast<size_t>(L.start + y * L.w + x) * MC) * VB) +
-                      static_cast<uint32_t>(kk * 16)
-                : kOobOffset;
-        unsigned char *dst = reinterpret_cast<unsigned char *>(vt) +
-                             static_cast<size_t>(wave * kWave + v * kTileBlock) * 16;
-        // cache policy 2 = non-temporal: a tile's value rows are staged once
-        // (c1 and c3 backward 1-3% faster, c2 unchanged)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            vrsrc, (__attribute__((address_space(3))) void *)dst, 16, off, 0, 0, 2);
-      }
+      const int cell = unit / UPV, kk = unit % UPV;
+      const int y = g.y_lo + cell / TV, x = g.x_lo + cell % TV;
+      const uint32_t off =
+          want && unit < NPOS * UPV && y < L.h && x < L.w
+              ? static_cast<uint32_t>(
+                    (slab + static_cast<size_t>(L.start + y * L.w + x) * MC) * VB) +
+                    static_cast<uint32_t>(kk * 16)
+              : kOobOffset;
+      // cache policy 2 = non-temporal: a tile's value rows are staged once
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(vrsrc, off, 0, 2);
+      vt_next[v] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  };
+  auto store_value_tile = [&]() {
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+      const int unit = tid + v * kTileBlock;
+      if (unit < NPOS * UPV) reinterpret_cast<uint4 *>(vt)[unit] = vt_next[v];
     }
   };
   // cell sums of a finished item's corner planes to grad_value (slots that
@@ -839,7 +849,8 @@ __global__ void __launch_bounds__(kTileBlock)
   uint4 r_cur[RPT];
 #pragma unroll
   for (int u = 0; u < RPT; ++u) r_cur[u] = load_record(c0, u);
-  stage_value_tile(c0.d);
+  load_value_tile(c0.d, true);
+  store_value_tile();
   if (tid < UPV) reinterpret_cast<uint4 *>(vt + NPOS * C)[tid] = make_uint4(0u, 0u, 0u, 0u);
   if (tid < C) dummy[tid] = 0.0f;
   if (tid < NPOS) pcount[tid] = 0;
@@ -862,7 +873,13 @@ __global__ void __launch_bounds__(kTileBlock)
     // round trip overlaps the batch
     const bool refill = moves_on(c1);
     uint32_t took = 0;
-    if (refill && tid == 0 && lo < hi) took = atomicAdd(queue, 1u);
+    // (mbcnt_lo(~0, 0) is 0 for thread 0; it makes the address look
+    // lane-dependent, so the compiler's atomic optimizer leaves this one-
+    // thread atomic alone instead of broadcasting its result -- and waiting
+    // for it, and for every earlier memory operation -- right here)
+    if (refill && tid == 0 && lo < hi) {
+      took = atomicAdd(queue + __builtin_amdgcn_mbcnt_lo(~0u, 0u), 1u);
+    }
 
     // A. next batch's records; this batch's sort keys. Record slots are
     // u * kTileBlock + tid; a wavefront whose first slot is past the batch
@@ -942,9 +959,8 @@ __global__ void __launch_bounds__(kTileBlock)
     lds_barrier();
     if (tid < NPOS) order[bstart[p_bk] + p_brank] = static_cast<uint32_t>(tid);
 
-    // C. records in position order; the value tile of a new item (copied by
-    // buffer-to-LDS loads issued in the previous batch) has landed once this
-    // thread's loads are done, and every thread's after the barrier
+    // C. records in position order; a new item's value tile (loaded into
+    // registers in the previous batch) into LDS
     uint32_t my_slot[RPT];
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
@@ -955,7 +971,7 @@ __global__ void __launch_bounds__(kTileBlock)
                                        __float_as_uint(my_wy1[u]), r_cur[u].w);
       }
     }
-    if (first_of_item) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) only
+    if (first_of_item) store_value_tile();
     lds_barrier();
 
     // D. owners: teams of S = 1, 2 or 4 lane groups (inside one 16-lane DPP
@@ -1088,10 +1104,11 @@ __global__ void __launch_bounds__(kTileBlock)
     lds_barrier();
 
     // E. the next batch's records move into place first (the empty asm
-    // pins the wait for their loads here, before this phase's stores and
-    // buffer-to-LDS loads are issued); then this batch's location/weight
-    // gradients over the records' slots, position counts reset, a finished
-    // item written back, the next item's value tile requested
+    // pins the wait for their loads here, before this phase's stores are
+    // issued); then this batch's location/weight gradients, the position
+    // counts reset, a finished item written back and, when the next batch
+    // starts an item, its value tile requested (into registers, waited for
+    // in that batch's phase C)
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
       r_cur[u] = r_next[u];
@@ -1125,7 +1142,7 @@ __global__ void __launch_bounds__(kTileBlock)
     if (tid < NPOS) pcount[tid] = 0;
     if (tid < kWave) bucket[tid] = 0;
     if (last_of_item) write_back(c0.d);
-    if (next_new_item) stage_value_tile(c1.d);
+    load_value_tile(c1.d, next_new_item);
     if (refill && tid == 0) taken[0] = lo + took < hi ? lo + took : kNoItem;
     c0 = c1;
     c1 = advance(c1);
