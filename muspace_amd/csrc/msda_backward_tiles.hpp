@@ -582,6 +582,25 @@ __device__ __forceinline__ void load8ch(const float *p, float (&o)[8]) {
 __device__ __forceinline__ void load8ch(const bf16_t *p, float (&o)[8]) { load16(p, o); }
 __device__ __forceinline__ void load8ch(const __half *p, float (&o)[8]) { load16(p, o); }
 
+// Eight channels at byte offset `off` of a buffer (32-bit offsets: fewer
+// address instructions than 64-bit pointers).
+template <typename VT>
+__device__ __forceinline__ void buffer_load8ch(__amdgpu_buffer_rsrc_t r, uint32_t off,
+                                               float (&o)[8]) {
+  if constexpr (sizeof(VT) == 4) {
+    float a[4], b[4];
+    decode16(VT(), buffer_load16(r, off), a);
+    decode16(VT(), buffer_load16(r, off + 16), b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[j] = a[j];
+      o[4 + j] = b[j];
+    }
+  } else {
+    decode16(VT(), buffer_load16(r, off), o);
+  }
+}
+
 // The four corner dot products of one record, D_d = sum over the group's KQ
 // lanes of dd[d], by a reduce-scatter across the group (each step halves the
 // values a lane carries), stored to the record's slot d4[0..3]. KQ = 4: lane k
@@ -643,7 +662,8 @@ template <typename VT, int C>
 __global__ void __launch_bounds__(kTileBlock)
     msda_tile_backward(const VT *__restrict__ value, uint32_t value_bytes,
                        const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
-                       const VT *__restrict__ grad_out, uint4 *__restrict__ records,
+                       const VT *__restrict__ grad_out, uint32_t grad_bytes,
+                       uint4 *__restrict__ records,
                        const Item *__restrict__ items, uint32_t *__restrict__ item_total,
                        Shape s, BinPlan p, float *__restrict__ grad_value,
                        float *__restrict__ grad_loc, float *__restrict__ grad_attn) {
@@ -685,6 +705,7 @@ __global__ void __launch_bounds__(kTileBlock)
   const int lane = tid % kWave, wave = tid / kWave;
   const int grp = tid / KQ, k = tid % KQ;
   const __amdgpu_buffer_rsrc_t vrsrc = make_rsrc(value, value_bytes);
+  const __amdgpu_buffer_rsrc_t grsrc = make_rsrc(grad_out, grad_bytes);
 
   // Items are taken dynamically: the list is cut into one contiguous share
   // per XCD (workgroups are dispatched to the XCDs round-robin, so block
@@ -967,8 +988,11 @@ __global__ void __launch_bounds__(kTileBlock)
       my_slot[u] = 0;
       if (wave_slot + u * kTileBlock < ns && pos[u] >= 0) {
         my_slot[u] = poff[pos[u]] + rank[u];
+        // the owners take the row weights with the attention weight folded
+        // in: {id, wx1, (1 - wy1) a, wy1 a}
         stash[my_slot[u]] = make_uint4(r_cur[u].x, __float_as_uint(my_wx1[u]),
-                                       __float_as_uint(my_wy1[u]), r_cur[u].w);
+                                       __float_as_uint((1.0f - my_wy1[u]) * my_a[u]),
+                                       __float_as_uint(my_wy1[u] * my_a[u]));
       }
     }
     if (first_of_item) store_value_tile();
@@ -983,12 +1007,14 @@ __global__ void __launch_bounds__(kTileBlock)
     // team (row_ror) and its last group writes the planes. The first batch of
     // an item visits every position (zero-count ones store zero sums); later
     // batches stop at the first empty position and add.
-    const VT *gbase =
-        grad_out + (static_cast<size_t>(b0) * s.queries * s.heads + m0) * C + k * CPL;
-    const uint32_t q_stride = static_cast<uint32_t>(s.heads * C);  // grad_out row stride
+    // grad_out rows through a buffer resource: byte offsets below 2^31
+    // (checked on the host), q < 2^24 and the row stride below 2^24 (24-bit
+    // multiply)
+    const uint32_t gbase = static_cast<uint32_t>(
+        ((static_cast<size_t>(b0) * s.queries * s.heads + m0) * C + k * CPL) * VB);
+    const uint32_t q_stride = static_cast<uint32_t>(s.heads * C * VB);  // grad_out row bytes
     const u32x4 *vstash = reinterpret_cast<const u32x4 *>(stash);
     float *stash_f = reinterpret_cast<float *>(stash);
-    // q < 2^24 and q * q_stride < 2^32 (checked on the host): a 24-bit multiply
     auto grow = [&](uint32_t id) {
       const uint32_t q =
           min((id & kSampleMask) >> p.lp_log2, static_cast<uint32_t>(s.queries - 1));
@@ -1025,9 +1051,8 @@ __global__ void __launch_bounds__(kTileBlock)
           load8ch(vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * C : NPOS * C) + k * CPL, v[d]);
         }
         auto one_record = [&](const u32x4 &e, const float (&gv)[CPL], uint32_t slot) {
-          const float wx1 = __uint_as_float(e.y), wy1 = __uint_as_float(e.z);
-          const float a = __uint_as_float(e.w);
-          const float ay0 = (1.0f - wy1) * a, ay1 = wy1 * a;
+          const float wx1 = __uint_as_float(e.y);
+          const float ay0 = __uint_as_float(e.z), ay1 = __uint_as_float(e.w);
           const float wx0 = 1.0f - wx1;
           const float wa[4] = {ay0 * wx0, ay0 * wx1, ay1 * wx0, ay1 * wx1};
           float dd[4];
@@ -1052,7 +1077,7 @@ __global__ void __launch_bounds__(kTileBlock)
 #pragma unroll
         for (int j = 0; j < NR; ++j) {
           e[j] = vstash[first + stride * min(static_cast<uint32_t>(j), cnt - 1)];
-          load8ch(grow(e[j].x), g[j]);
+          buffer_load8ch<VT>(grsrc, grow(e[j].x), g[j]);
         }
         for (uint32_t r = 0; r < cnt; r += NR) {
 #pragma unroll
@@ -1061,7 +1086,7 @@ __global__ void __launch_bounds__(kTileBlock)
             const uint32_t nx = r + j + NR;
             const u32x4 t = vstash[first + stride * min(nx, cnt - 1)];
             e[j] = nx < cnt ? t : e[j];
-            load8ch(grow(e[j].x), g[j]);
+            buffer_load8ch<VT>(grsrc, grow(e[j].x), g[j]);
           }
         }
       }

@@ -640,6 +640,11 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   // the tile kernel stages value tiles with 32-bit buffer offsets below kOobOffset
   const size_t vb = value_dtype == MUSPACE_DTYPE_F32 ? 4 : 2;
   if (value_bytes(s, vb) + 64 > msda::kOobOffset) return false;
+  // ... and reads grad_out rows with 32-bit buffer offsets below kOobOffset
+  if (static_cast<size_t>(s.batch) * s.queries * s.heads * s.channels * vb + 64 >
+      msda::kOobOffset) {
+    return false;
+  }
   if (static_cast<int64_t>(s.queries) * s.heads * s.channels >= (int64_t{1} << 32)) return false;
   p.rec_cap = static_cast<int64_t>(s.queries) * s.lp;
   // Direct gradient writes scatter 12 bytes per sample over the slab's span of
@@ -729,8 +734,11 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   }
   if (phase == Phase::kBin) return;
   const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
-  tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, vbytes, shapes, starts, go, records, items,
-                                                          item_total, s, p, gv, gl, ga);
+  const uint32_t gbytes = static_cast<uint32_t>(static_cast<size_t>(s.batch) * s.queries *
+                                                s.heads * C * sizeof(VT));
+  tile<<<tile_grid(), msda::kTileBlock, tile_bytes, st>>>(v, vbytes, shapes, starts, go, gbytes,
+                                                          records, items, item_total, s, p, gv,
+                                                          gl, ga);
   if (!p.direct) {
     const int per_slab = static_cast<int>((p.rec_cap + msda::kBinBlock - 1) / msda::kBinBlock);
     msda::msda_grad_gather<<<bm * per_slab, msda::kBinBlock, 0, st>>>(rec_of_sample, records, s,
