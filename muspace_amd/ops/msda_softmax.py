@@ -20,6 +20,8 @@ Gradients, dtypes and the early binning on a side stream follow
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from ..runtime.kernel_dispatch import (
@@ -33,6 +35,7 @@ from ..runtime.native import native_error
 from .multi_scale_deformable_attn import (
     _bins_early,
     _native_extension,
+    _reserve_early_buffers,
     _native_geometry_dtype,
     _side_stream,
     _validate_inputs,
@@ -52,8 +55,15 @@ def attention_softmax(attention_logits: torch.Tensor) -> torch.Tensor:
 
 def _start_binning(ext, value, spatial, starts, sampling, logits, im2col_step):
     """Workspace, gradients and the backward's first part (probabilities and
-    binning) on a side stream, ordered after the work that produced the inputs."""
+    binning) on a side stream, ordered after the work that produced the inputs.
+    None when the early-binning budget is spent (the backward then runs in one
+    call)."""
+    release = _reserve_early_buffers(ext.backward_softmax_workspace_bytes(value, sampling),
+                                     value, sampling, logits)
+    if release is None:
+        return None
     workspace = ext.backward_softmax_workspace(value, sampling)
+    weakref.finalize(workspace, release)
     device = value.device
     grads = (
         torch.empty(value.shape, dtype=torch.float32, device=device),

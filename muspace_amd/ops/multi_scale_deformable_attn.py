@@ -31,7 +31,9 @@ cast to the value dtype before grid_sample).
 from __future__ import annotations
 
 import os
+import threading
 import warnings
+import weakref
 
 import torch
 import torch.nn.functional as F
@@ -132,10 +134,74 @@ def _native_geometry_dtype(value: torch.Tensor, *geometry: torch.Tensor) -> torc
 
 # Early binning: the tile-owned backward's binning reads only the geometry, so
 # the forward starts it on a second stream where it overlaps the forward
-# kernel (c2 step 1255 -> 1204 us measured). The backward's buffers then live
-# from the forward to the backward; MUSPACE_EARLY_BINNING=0 turns this off.
+# kernel (c2 step 1255 -> 1204 us measured). The backward's buffers (its
+# scratch and the three float32 gradients) then live from the forward to the
+# backward; MUSPACE_EARLY_BINNING=0 turns this off, and a per-device byte
+# budget bounds what all forwards awaiting their backward may hold
+# (MUSPACE_EARLY_BINNING_BUDGET bytes, default 1/32 of the device's memory):
+# a forward that would exceed it does not bin early.
 EARLY_BINNING_ENV = "MUSPACE_EARLY_BINNING"
+EARLY_BINNING_BUDGET_ENV = "MUSPACE_EARLY_BINNING_BUDGET"
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+class BinningBudget:
+    """Bytes held by early binning per device, against a limit.
+
+    A forward reserves its buffers' bytes before allocating them and the
+    reservation is returned when its scratch tensor is freed (after the
+    backward consumed it, or when the graph is dropped without a backward).
+    """
+
+    def __init__(self, limit_of=None) -> None:
+        self._held: dict[int, int] = {}
+        self._limits: dict[int, int] = {}
+        self._lock = threading.Lock()
+        self._limit_of = limit_of or self._device_limit
+
+    @staticmethod
+    def _device_limit(index: int) -> int:
+        raw = os.environ.get(EARLY_BINNING_BUDGET_ENV, "").strip()
+        if raw:
+            return int(raw)
+        return torch.cuda.get_device_properties(index).total_memory // 32
+
+    def held(self, index: int) -> int:
+        with self._lock:
+            return self._held.get(index, 0)
+
+    def try_reserve(self, index: int, nbytes: int) -> bool:
+        with self._lock:
+            limit = self._limits.get(index)
+            if limit is None:
+                limit = self._limits[index] = self._limit_of(index)
+            held = self._held.get(index, 0)
+            if held + nbytes > limit:
+                return False
+            self._held[index] = held + nbytes
+            return True
+
+    def release(self, index: int, nbytes: int) -> None:
+        with self._lock:
+            self._held[index] = self._held.get(index, 0) - nbytes
+
+
+binning_budget = BinningBudget()
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def _reserve_early_buffers(workspace_bytes: int, *like: torch.Tensor):
+    """Reserve the budget for a workspace of `workspace_bytes` and float32
+    gradients shaped like `like`; returns a release callback or None."""
+    device = like[0].device
+    nbytes = workspace_bytes + 4 * sum(t.numel() for t in like)
+    index = _device_index(device)
+    if not binning_budget.try_reserve(index, nbytes):
+        return None
+    return lambda: binning_budget.release(index, nbytes)
 
 
 def _early_binning_enabled() -> bool:
@@ -151,7 +217,7 @@ def _bins_early(*tensors: torch.Tensor) -> bool:
 
 
 def _side_stream(device: torch.device) -> torch.cuda.Stream:
-    index = device.index if device.index is not None else torch.cuda.current_device()
+    index = _device_index(device)
     stream = _SIDE_STREAMS.get(index)
     if stream is None:
         stream = torch.cuda.Stream(device=index)  # default priority
@@ -163,10 +229,15 @@ def _start_binning(ext, value, spatial, starts, sampling, attn, im2col_step):
     """Allocate the backward's workspace and gradients and run its binning on a
     side stream, ordered after the work that produced the inputs. Returns the
     buffers and the completion event, or None when the shape takes the atomic
-    backward (nothing to bin)."""
-    workspace = ext.backward_workspace(value, sampling)
-    if workspace.numel() <= 1:
+    backward (nothing to bin) or the early-binning budget is spent."""
+    nbytes = ext.backward_workspace_bytes(value, sampling)
+    if nbytes <= 1:
         return None
+    release = _reserve_early_buffers(nbytes, value, sampling, attn)
+    if release is None:
+        return None
+    workspace = ext.backward_workspace(value, sampling)
+    weakref.finalize(workspace, release)
     device = value.device
     grads = (
         torch.empty(value.shape, dtype=torch.float32, device=device),

@@ -200,6 +200,8 @@ class NativeLibrary:
             "ms_deform_attn_backward": self.ms_deform_attn_backward,
             "ms_deform_attn_backward_noalloc": self.ms_deform_attn_backward_noalloc,
             "backward_workspace": self.backward_workspace,
+            "backward_workspace_bytes": self.backward_workspace_bytes,
+            "backward_softmax_workspace_bytes": self.backward_softmax_workspace_bytes,
             "ms_deform_attn_backward_bin": self.ms_deform_attn_backward_bin,
             "ms_deform_attn_backward_rest": self.ms_deform_attn_backward_rest,
             "ms_deform_attn_forward_softmax": self.ms_deform_attn_forward_softmax,
@@ -429,6 +431,15 @@ class NativeLibrary:
                 heads, channels, levels, queries, points))
         return int(self._raw["ms_deform_attn_backward_workspace_size"](
             _dtype_code(value.dtype), batch, spatial, heads, channels, levels, queries, points))
+
+    def backward_workspace_bytes(self, value, sampling_locations) -> int:
+        """Scratch bytes of the tile-owned backward for these shapes (0: the
+        shape takes the atomic fallback)."""
+        return self._workspace_bytes(value, sampling_locations, softmax=False)
+
+    def backward_softmax_workspace_bytes(self, value, sampling_locations) -> int:
+        """Scratch bytes of the softmax backward for these shapes."""
+        return self._workspace_bytes(value, sampling_locations, softmax=True)
 
     def backward_workspace(self, value, sampling_locations):
         """Scratch of the tile-owned backward for these shapes (1 byte when the

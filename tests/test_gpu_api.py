@@ -48,7 +48,9 @@ class _NativeCallSpy:
 
         def recorded(*args, **kwargs):
             # size queries and argument checks are not kernel entry points
-            if name not in {"backward_workspace", "check_forward", "check_backward"}:
+            if name not in {"backward_workspace", "backward_workspace_bytes",
+                            "backward_softmax_workspace_bytes", "check_forward",
+                            "check_backward"}:
                 self.calls.append((name, [getattr(arg, "dtype", None) for arg in args]))
             return target(*args, **kwargs)
 
@@ -266,3 +268,31 @@ def test_split_backward_entry_points_match_the_one_call(embed_dims):
     lib.ms_deform_attn_backward_rest(value, shapes, starts, loc, attn, grad, *got, 64, ws)
     for a, b in zip(got, ref):
         torch.testing.assert_close(a, b, rtol=1e-6, atol=1e-6)
+
+
+def test_early_binning_reservation_is_returned_after_the_backward(monkeypatch):
+    """The bytes a forward reserves for its early-binned backward buffers are
+    returned once the backward has consumed them, and a forward over the
+    budget runs without early binning and still gets the same gradients."""
+    monkeypatch.setenv("MUSPACE_EARLY_BINNING", "1")
+    budget = msda_module.binning_budget
+    index = torch.cuda.current_device()
+    before = budget.held(index)
+    tensors = _fixture(device=DEV, batch=2, queries=96, heads=2, embed_dims=32,
+                       levels=((8, 12), (4, 6)), points=4)
+    out = multi_scale_deformable_attn(*tensors, backend="hip")
+    assert budget.held(index) > before  # the backward's buffers are held
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(5)).to(DEV)
+    out.backward(g)
+    del out
+    assert budget.held(index) == before
+    early = [t.grad.clone() for t in (tensors[0], tensors[3], tensors[4])]
+    for t in (tensors[0], tensors[3], tensors[4]):
+        t.grad = None
+    tight = msda_module.BinningBudget(limit_of=lambda i: 0)
+    monkeypatch.setattr(msda_module, "binning_budget", tight)
+    out = multi_scale_deformable_attn(*tensors, backend="hip")
+    assert tight.held(index) == 0
+    out.backward(g)
+    for a, t in zip(early, (tensors[0], tensors[3], tensors[4])):
+        torch.testing.assert_close(t.grad, a, rtol=1e-6, atol=1e-6)

@@ -230,3 +230,33 @@ def test_gradient_buffer_on_another_device_is_rejected(native_lib, raw_launches)
     gl = gl.to("meta")  # a device other than the value's
     with pytest.raises(RuntimeError, match="grad_sampling_locations is on meta"):
         native_lib.check_backward(value, shapes, starts, loc, attn, None, gv, gl, ga)
+
+
+# ------------------------------------------------- early-binning budget ---
+
+
+def test_binning_budget_reserves_up_to_its_limit_and_releases():
+    budget = msda_module.BinningBudget(limit_of=lambda index: 100)
+    assert budget.try_reserve(0, 60)
+    assert not budget.try_reserve(0, 50)  # 110 > 100: no early binning
+    assert budget.try_reserve(1, 90)  # per device
+    budget.release(0, 60)
+    assert budget.try_reserve(0, 100)
+    assert budget.held(0) == 100 and budget.held(1) == 90
+
+
+def test_reservations_over_the_budget_are_refused(monkeypatch):
+    """A forward whose buffers would exceed the budget gets no reservation
+    (it then does not bin early); releasing one makes room again."""
+    budget = msda_module.BinningBudget(limit_of=lambda index: 1 << 20)
+    monkeypatch.setattr(msda_module, "binning_budget", budget)
+    monkeypatch.setattr(msda_module, "_device_index", lambda device: 0)
+    value, shapes, starts, loc, attn = _inputs()
+    need = 4 * (value.numel() + loc.numel() + attn.numel()) + 4096
+    assert budget.try_reserve(0, (1 << 20) - need + 1)
+    assert msda_module._reserve_early_buffers(4096, value, loc, attn) is None
+    budget.release(0, (1 << 20) - need + 1)
+    release = msda_module._reserve_early_buffers(4096, value, loc, attn)
+    assert release is not None and budget.held(0) == need
+    release()
+    assert budget.held(0) == 0
