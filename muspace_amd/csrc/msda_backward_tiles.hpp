@@ -238,7 +238,7 @@ __global__ void __launch_bounds__(kBinBlock)
   // samples per thread in flight (every load unconditional, clamped index)
   const int lpp = 1 << p.lp_log2;
   const int total = nq * lpp;
-  constexpr int U = 8;
+  constexpr int U = 16;
   for (int i0 = threadIdx.x; i0 < total; i0 += kBinBlock * U) {
     float lx[U], ly[U];
     bool live[U];
@@ -298,13 +298,26 @@ __global__ void __launch_bounds__(kBinBlock)
   uint32_t *ts = tile_start + static_cast<size_t>(bm) * (p.tile_bound + 1);
   if (threadIdx.x == 0) zero_count = 0;
 
-  // each thread owns a contiguous run of tiles
+  // each thread owns a contiguous run of tiles. The per-chunk counts are
+  // read kScanBlock at a time, all loads of a block before its stores (a
+  // load after a store to the same array could not be moved ahead of it, and
+  // the read-modify-write per chunk was one memory round trip each).
+  constexpr int kScanBlock = 16;
   const int per = (nt + kBinBlock - 1) / kBinBlock;
   const int t0 = min(nt, static_cast<int>(threadIdx.x) * per), t1 = min(nt, t0 + per);
   uint32_t run = 0;
   for (int t = t0; t < t1; ++t) {
     uint32_t tot = 0;
-    for (int c = 0; c < p.chunks; ++c) tot += cnt[static_cast<size_t>(c) * p.tile_bound + t];
+    for (int c0 = 0; c0 < p.chunks; c0 += kScanBlock) {
+      uint32_t v[kScanBlock];
+#pragma unroll
+      for (int j = 0; j < kScanBlock; ++j) {
+        const int c = min(c0 + j, p.chunks - 1);
+        v[j] = cnt[static_cast<size_t>(c) * p.tile_bound + t];
+      }
+#pragma unroll
+      for (int j = 0; j < kScanBlock; ++j) tot += c0 + j < p.chunks ? v[j] : 0u;
+    }
     ts[t] = tot;  // the tile's record count until it is replaced by its offset
     run += tot;
   }
@@ -315,11 +328,20 @@ __global__ void __launch_bounds__(kBinBlock)
     const uint32_t n = ts[t];
     ts[t] = off;
     uint32_t cur = off;
-    for (int c = 0; c < p.chunks; ++c) {
-      uint32_t *x = &cnt[static_cast<size_t>(c) * p.tile_bound + t];
-      const uint32_t v = *x;
-      *x = cur;
-      cur += v;
+    for (int c0 = 0; c0 < p.chunks; c0 += kScanBlock) {
+      uint32_t v[kScanBlock];
+#pragma unroll
+      for (int j = 0; j < kScanBlock; ++j) {
+        const int c = min(c0 + j, p.chunks - 1);
+        v[j] = cnt[static_cast<size_t>(c) * p.tile_bound + t];
+      }
+#pragma unroll
+      for (int j = 0; j < kScanBlock; ++j) {
+        if (c0 + j < p.chunks) {
+          cnt[static_cast<size_t>(c0 + j) * p.tile_bound + t] = cur;
+          cur += v[j];
+        }
+      }
     }
     off += n;
   }
