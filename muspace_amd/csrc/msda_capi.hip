@@ -125,12 +125,20 @@ Launch plan_rows(const msda::Shape &s, int kq, int max_ns) {
   const int need = (s.lp + gu - 1) / gu;
   Launch L;
   L.ns = need <= 1 ? 1 : (need <= 2 ? 2 : 4);
-  if (max_ns >= 8 && kq >= 8 && s.lp >= 32) {
-    // eight samples per lane group and step (32 corner gathers in flight per
-    // group; measured 4% faster than four at the BEVFormer shape)
-    L.ns = 8;
-    gu = pow2_ceil((s.lp + 7) / 8);
-    if (gu > ng) gu = ng;
+  if (max_ns >= 8) {
+    // forward: as many samples per lane group and step as the lane group has
+    // lanes for taps, up to 8 (4 * NS corner gathers in flight per group and
+    // fewer groups to reduce over per unit). Measured against the smallest NS
+    // that covers a unit with at most 64/KQ groups: NS 8 for L*P >= 16 and
+    // 4 for L*P >= 4 took the forward at c1 from 178 to 140 us, c3 from 133
+    // to 105 us and c4 bf16 (KQ = 4) from 1058 to 882 us; at c2 (L*P = 32)
+    // 8 was already chosen.
+    const int ns = (kq >= 8 && s.lp >= 16) ? 8 : (kq >= 4 && s.lp >= 4) ? 4 : 0;
+    if (ns > L.ns) {
+      L.ns = ns;
+      gu = pow2_ceil((s.lp + ns - 1) / ns);
+      if (gu > ng) gu = ng;
+    }
   }
   if (L.ns > kq) L.ns = kq;  // the forward computes one tap per lane: ng * ns <= 64
   L.plan.gu_log2 = log2_int(gu);
