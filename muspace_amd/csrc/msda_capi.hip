@@ -118,14 +118,14 @@ struct Launch {
   int blocks;
 };
 
-Launch plan_rows(const msda::Shape &s, int kq, int max_ns) {
+Launch plan_rows(const msda::Shape &s, int kq, int max_ns, bool forward) {
   const int ng = msda::kWave / kq;
   int gu = pow2_ceil(s.lp > 0 ? s.lp : 1);
   if (gu > ng) gu = ng;
   const int need = (s.lp + gu - 1) / gu;
   Launch L;
   L.ns = need <= 1 ? 1 : (need <= 2 ? 2 : 4);
-  if (max_ns >= 8) {
+  if (forward) {
     // forward: as many samples per lane group and step as the lane group has
     // lanes for taps, up to 8 (4 * NS corner gathers in flight per group and
     // fewer groups to reduce over per unit). Measured against the smallest NS
@@ -133,7 +133,7 @@ Launch plan_rows(const msda::Shape &s, int kq, int max_ns) {
     // 4 for L*P >= 4 took the forward at c1 from 178 to 140 us, c3 from 133
     // to 105 us and c4 bf16 (KQ = 4) from 1058 to 882 us; at c2 (L*P = 32)
     // 8 was already chosen.
-    const int ns = (kq >= 8 && s.lp >= 16) ? 8 : (kq >= 4 && s.lp >= 4) ? 4 : 0;
+    const int ns = (kq >= 8 && max_ns >= 8 && s.lp >= 16) ? 8 : (kq >= 4 && s.lp >= 4) ? 4 : 0;
     if (ns > L.ns) {
       L.ns = ns;
       gu = pow2_ceil((s.lp + ns - 1) / ns);
@@ -141,6 +141,7 @@ Launch plan_rows(const msda::Shape &s, int kq, int max_ns) {
     }
   }
   if (L.ns > kq) L.ns = kq;  // the forward computes one tap per lane: ng * ns <= 64
+  if (L.ns > max_ns) L.ns = max_ns;
   L.plan.gu_log2 = log2_int(gu);
   L.plan.iters = 8;  // units per lane group: the next unit's geometry loads overlap the gathers
   const int64_t units_per_wave_iter = ng / gu;
@@ -186,7 +187,9 @@ bool rows_aligned(std::initializer_list<const void *> ptrs16, const void *ptr8 =
 template <typename VT, int C, typename Go>
 void forward_rows_ns(const msda::Shape &s, Go &&go) {
   constexpr int KQ = C / msda::RowTraits<VT>::kCpl;
-  const Launch L = plan_rows(s, KQ, 8);
+  // 16-bit C = 64 rows at NS = 8 need more than 256 VGPRs (one wavefront per
+  // SIMD and AGPR spills): four samples per step there
+  const Launch L = plan_rows(s, KQ, sizeof(VT) == 2 && C >= 64 ? 4 : 8, true);
   switch (L.ns) {
     case 1:
       go(std::integral_constant<int, 1>(), L);
@@ -513,7 +516,7 @@ void launch_backward_rows(const void *value, const int64_t *shapes, const int64_
                           const void *loc, const void *attn, const void *grad_out, float *gv,
                           float *gl, float *ga, const msda::Shape &s, hipStream_t st) {
   constexpr int KQ = C / msda::RowTraits<VT>::kCpl;
-  const Launch L = plan_rows(s, KQ, 4);
+  const Launch L = plan_rows(s, KQ, 4, false);
   const VT *v = static_cast<const VT *>(value);
   const GT *lc = static_cast<const GT *>(loc);
   const GT *aw = static_cast<const GT *>(attn);
