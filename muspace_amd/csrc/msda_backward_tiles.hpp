@@ -1029,6 +1029,14 @@ __global__ void __launch_bounds__(kTileBlock)
     // team (row_ror) and its last group writes the planes. The first batch of
     // an item visits every position (zero-count ones store zero sums); later
     // batches stop at the first empty position and add.
+    // When the batch uses single-group teams, wavefront 0 -- which holds the
+    // largest positions, and whose chain of grad_out loads bounds the phase --
+    // works in teams of two instead (its 8 teams take ranks 0-7 of a round,
+    // the other wavefronts' groups the ranks after them). Wavefront-uniform,
+    // so the team sum stays one DPP pass per wavefront. Measured against
+    // single groups everywhere: c2 tile kernel 616 -> 588 us, c4 bf16 1600
+    // -> 1543 us; a first wavefront of 4-group teams, or two wavefronts of
+    // 2-group teams, gained less.
     // grad_out rows through a buffer resource: byte offsets below 2^31
     // (checked on the host), q < 2^24 and the row stride below 2^24 (24-bit
     // multiply)
@@ -1042,9 +1050,20 @@ __global__ void __launch_bounds__(kTileBlock)
           min((id & kSampleMask) >> p.lp_log2, static_cast<uint32_t>(s.queries - 1));
       return gbase + __umul24(q, q_stride);
     };
-    const int tshift = team_shift_s;
-    const int S = 1 << tshift, NT = NG >> tshift;
-    const int team = grp >> tshift, sub = grp & (S - 1);
+    int tshift = team_shift_s;
+    int NT = NG >> tshift, team = grp >> tshift;
+    if (tshift == 0) {
+      constexpr int GPW = kWave / KQ;  // lane groups per wavefront
+      if (__builtin_amdgcn_readfirstlane(wave) == 0) {
+        tshift = 1;
+        team = grp >> 1;
+      } else {
+        team = grp - GPW / 2;
+      }
+      NT = NG - GPW / 2;
+    }
+    const int S = 1 << tshift;
+    const int sub = grp & (S - 1);
 #pragma unroll 1
     for (int rnd = 0; rnd * NT < NPOS; ++rnd) {
       const int i = rnd * NT + ((rnd & 1) ? NT - 1 - team : team);
