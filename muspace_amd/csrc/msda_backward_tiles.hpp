@@ -114,7 +114,7 @@ __host__ __device__ constexpr size_t tile_lds_bytes() {
   return static_cast<size_t>(NPOS + 1) * C * sizeof(VT) +  // value tile + halo, zero row
          static_cast<size_t>(4 * NPOS) * C * 4 +           // corner planes
          static_cast<size_t>(K) * 16 +                     // sorted records
-         static_cast<size_t>(3 * NPOS) * 4 +               // position count, offset, order
+         static_cast<size_t>(4 * NPOS) * 4 +               // position count, offset, rank table
          2 * 64 * 4 +                                      // count buckets, bucket starts
          16 * 4 +                                          // per-wavefront count totals
          static_cast<size_t>(C) * 4;                       // zero slot
@@ -703,6 +703,7 @@ __global__ void __launch_bounds__(kTileBlock)
   constexpr int kMaxTeamShift = KQ <= 4 ? 2 : 1;
   static_assert(CPL == 8 && (KQ == 2 || KQ == 4 || KQ == 8), "bad lane layout");
   static_assert(K % kTileBlock == 0 && NPOS <= kTileBlock, "bad batch size");
+  static_assert(K < 65536 && NPOS < 65536, "rank table packs count and position in 16 bits");
   static_assert(tile_lds_bytes<VT, C>() + 3400 <= kTileLdsLimit, "tile LDS budget");
 
   __shared__ Level lv[kMaxLevels];
@@ -715,8 +716,9 @@ __global__ void __launch_bounds__(kTileBlock)
   float *dummy = reinterpret_cast<float *>(stash + K);  // [C], always zero (16-byte aligned)
   uint32_t *pcount = reinterpret_cast<uint32_t *>(dummy + C);
   uint32_t *poff = pcount + NPOS;
-  uint32_t *order = poff + NPOS;
-  uint32_t *bucket = order + NPOS;  // [64] positions per count bucket
+  // rank table: rank r -> {count << 16 | position, first slot}
+  uint2 *rtab = reinterpret_cast<uint2 *>(poff + NPOS);
+  uint32_t *bucket = reinterpret_cast<uint32_t *>(rtab + NPOS);  // [64] positions per count bucket
   uint32_t *bstart = bucket + 64;   // [64] first rank of each bucket
   uint32_t *wsum = bstart + 64;     // [16] counts per wavefront of positions
 
@@ -976,10 +978,12 @@ __global__ void __launch_bounds__(kTileBlock)
       }
     }
     lds_barrier();
+    uint32_t p_off = 0;
     if (tid < NPOS) {
       uint32_t before = 0;
       for (int w = 0; w < wave; ++w) before += wsum[w];
-      poff[tid] = before + p_incl - p_cnt;
+      p_off = before + p_incl - p_cnt;
+      poff[tid] = p_off;
     }
     if (tid < kWave) {
       const uint32_t v = bucket[tid];
@@ -1000,7 +1004,9 @@ __global__ void __launch_bounds__(kTileBlock)
       }
     }
     lds_barrier();
-    if (tid < NPOS) order[bstart[p_bk] + p_brank] = static_cast<uint32_t>(tid);
+    if (tid < NPOS) {
+      rtab[bstart[p_bk] + p_brank] = make_uint2((p_cnt << 16) | static_cast<uint32_t>(tid), p_off);
+    }
 
     // C. records in position order; a new item's value tile (loaded into
     // registers in the previous batch) into LDS
@@ -1068,8 +1074,9 @@ __global__ void __launch_bounds__(kTileBlock)
     for (int rnd = 0; rnd * NT < NPOS; ++rnd) {
       const int i = rnd * NT + ((rnd & 1) ? NT - 1 - team : team);
       if (i >= NPOS) break;  // later rounds start further out
-      const int p_id = static_cast<int>(order[i]);
-      const uint32_t n = pcount[p_id];
+      const uint2 rt = rtab[i];  // one LDS read: position, its count and first slot
+      const int p_id = static_cast<int>(rt.x & 0xffffu);
+      const uint32_t n = rt.x >> 16;
       if (n == 0 && !first_of_item) break;  // positions are in order of decreasing count
       float acc[4][CPL];
 #pragma unroll
@@ -1081,7 +1088,7 @@ __global__ void __launch_bounds__(kTileBlock)
                                ? (n - static_cast<uint32_t>(sub) + S - 1) >> tshift
                                : 0u;
       if (cnt > 0) {
-        const uint32_t first = poff[p_id] + static_cast<uint32_t>(sub);
+        const uint32_t first = rt.y + static_cast<uint32_t>(sub);
         const uint32_t stride = static_cast<uint32_t>(S);
         const int py = p_id / TV - 1, px = p_id % TV - 1;  // tile frame, >= -1
         // corner value rows (row -1 or column -1: the zero row after the tile)
