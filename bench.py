@@ -140,7 +140,9 @@ def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True,
     repeats), each bracketed by device synchronisation and HIP events on the
     main stream; ms_per_step is the median of the repeats' per-step means
     (the reference's protocol, /root/reference/benchmarks/_harness.py:226-260),
-    with the overall mean beside it. Inside the timed region HIP events sit
+    with the overall mean beside it. rest_ms is likewise the median over the
+    repeats of the repeat's mean rest-of-backward time, so one disturbed
+    repeat moves neither figure. Inside the timed region HIP events sit
     only around the rest of the backward (the roofline's kernel) on the main
     stream: each pair of events costs about 10 us a step, and a pair around
     the forward also delays its overlap with the binning. The forward's, the
@@ -172,7 +174,7 @@ def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True,
         start.record(stream)
         for _ in range(n):
             if per_kernel:
-                marks.append({})
+                marks.append({"repeat": len(samples)})
                 step.run(timed)
             else:
                 step.run()
@@ -188,7 +190,11 @@ def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True,
     if per_kernel:
         def avg(a, b):
             return sum(m[a].elapsed_time(m[b]) for m in marks) / len(marks)
-        res["rest_ms"] = avg("rest0", "rest1")
+        per_repeat = {}
+        for m in marks:
+            per_repeat.setdefault(m["repeat"], []).append(m["rest0"].elapsed_time(m["rest1"]))
+        res["rest_ms"] = statistics.median(statistics.fmean(v) for v in per_repeat.values())
+        res["repeat_rest_ms"] = [round(statistics.fmean(v), 4) for _, v in sorted(per_repeat.items())]
         marks.clear()
         extra = marker({"fwd0", "fwd1", "bin0", "bin1", "alloc0", "alloc1"})
         for _ in range(max(3, min(steps, 10))):
@@ -764,6 +770,7 @@ def main() -> int:
         "ms_per_step": round(res["ms_per_step"], 4),
         "timing": {"repeats": len(res["repeat_ms_per_step"]), "statistic": "median of repeats",
                    "repeat_ms_per_step": res["repeat_ms_per_step"],
+                   "repeat_rest_ms": res["repeat_rest_ms"],
                    "mean_ms_per_step": round(res["mean_ms_per_step"], 4)},
         "higher_is_better": True,
         "scaling": "weak",
