@@ -63,13 +63,17 @@ TRAFFIC_FILE = ROOT / "profiles" / "traffic_c2_fp32.json"
 class Step:
     """Preallocated inputs of one config and the launches of one step.
 
-    As the operator's autograd function does: the gradient buffers and the
-    backward's workspace are allocated first, the backward's binning (it reads
-    only the geometry) runs on a second stream while the forward runs, and the
-    rest of the backward follows on the main stream once grad_output is there.
+    As the operator's autograd function does (binning="fused"): the gradient
+    buffers and the backward's workspace are allocated first, one call runs
+    the forward together with the backward's binning (the forward kernel stores
+    the backward's records), and the rest of the backward follows once
+    grad_output is there. binning="side" is the earlier schedule kept for
+    comparison: the three binning kernels on a second stream beside the
+    forward kernel; "serial" runs them on the main stream before it (for
+    per-kernel profiles).
     """
 
-    def __init__(self, lib, cfg, value_dtype, geometry_dtype, device, serial=False):
+    def __init__(self, lib, cfg, value_dtype, geometry_dtype, device, binning="fused"):
         t = make_inputs(cfg, value_dtype=value_dtype, geometry_dtype=geometry_dtype, device=device)
         self.lib = lib
         self.value = t["value"]
@@ -79,8 +83,9 @@ class Step:
         self.attn = t["attention_weights"]
         self.grad = t["grad_output"]
         self.out_shape = (cfg.batch, cfg.queries, cfg.heads * cfg.channels)
-        # default priority; `serial` bins on the main stream (for per-kernel profiles)
-        self.side = torch.cuda.current_stream() if serial else torch.cuda.Stream()
+        self.binning = binning
+        # default priority
+        self.side = torch.cuda.Stream() if binning == "side" else torch.cuda.current_stream()
 
     def alloc(self):
         dev = self.value.device
@@ -101,6 +106,13 @@ class Step:
                                         self.attn, out, 64)
         return out
 
+    def forward_bin(self, bufs):
+        gv, gl, ga, ws = bufs
+        out = torch.empty(self.out_shape, dtype=self.value.dtype, device=self.value.device)
+        self.lib.ms_deform_attn_forward_bin(self.value, self.shapes, self.starts, self.loc,
+                                            self.attn, out, gv, gl, ga, 64, ws)
+        return out
+
     def rest(self, bufs):
         gv, gl, ga, ws = bufs
         self.lib.ms_deform_attn_backward_rest(self.value, self.shapes, self.starts, self.loc,
@@ -114,6 +126,14 @@ class Step:
         mark("alloc0", main)
         bufs = self.alloc()
         mark("alloc1", main)
+        if self.binning == "fused":
+            mark("fwd0", main)
+            self.forward_bin(bufs)
+            mark("fwd1", main)
+            mark("rest0", main)
+            self.rest(bufs)
+            mark("rest1", main)
+            return
         ready = torch.cuda.Event()
         ready.record(main)
         self.side.wait_event(ready)
@@ -202,7 +222,8 @@ def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True,
             step.run(extra)
         torch.cuda.synchronize()
         res["fwd_ms"] = avg("fwd0", "fwd1")
-        res["bin_ms"] = avg("bin0", "bin1")
+        # fused: the binning is part of the forward call
+        res["bin_ms"] = avg("bin0", "bin1") if step.binning != "fused" else 0.0
         res["zero_ms"] = avg("alloc0", "alloc1")
         res["bwd_ms"] = res["bin_ms"] + res["rest_ms"]
     return res
@@ -655,7 +676,8 @@ def main() -> int:
     parser.add_argument("--softmax-only", action="store_true",
                         help="only the fused attention-softmax leg (c2)")
     parser.add_argument("--serial-backward", action="store_true",
-                        help="bin on the main stream (no overlap with the forward), so that "
+                        help="time the earlier schedule with its three binning kernels on "
+                             "the main stream before the plain forward kernel, so that "
                              "rocprofv3 sees each kernel alone")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="only run a device-to-device copy of this many MiB, 5 times "
@@ -705,7 +727,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
     print(f"[bench] inputs for {cfg.name}", file=sys.stderr, flush=True)
-    step = Step(lib, cfg, torch.float32, torch.float32, dev, serial=args.serial_backward)
+    step = Step(lib, cfg, torch.float32, torch.float32, dev,
+                binning="serial" if args.serial_backward else "fused")
     res = time_steps(step, args.steps, args.warmup, repeats=args.repeats)
     fwd_b, bwd_b = algorithmic_bytes(cfg)
     gbps = (fwd_b + bwd_b) / (res["ms_per_step"] * 1e-3) / 1e9
@@ -721,18 +744,35 @@ def main() -> int:
             print(f"[bench] extra {name} {vdt}", file=sys.stderr, flush=True)
             s = Step(lib, c, vdt, torch.float32, dev)
             r = time_steps(s, 50, 10)
+            del s
+            # the earlier schedule: three binning kernels on a second stream
+            s = Step(lib, c, vdt, torch.float32, dev, binning="side")
+            r_side = time_steps(s, 50, 10)
+            del s
             f, b = algorithmic_bytes(c, vdt)
             extra[f"{name}-{str(vdt).replace('torch.', '')}"] = {
                 "fwd_bwd_us": round(r["ms_per_step"] * 1e3, 1),
                 "fwd_us": round(r["fwd_ms"] * 1e3, 1),
                 "bwd_us": round(r["bwd_ms"] * 1e3, 1),
-                "bin_us": round(r["bin_ms"] * 1e3, 1),
                 "rest_us": round(r["rest_ms"] * 1e3, 1),
                 "alloc_us": round(r["zero_ms"] * 1e3, 1),
                 "effective_GBps": round((f + b) / (r["ms_per_step"] * 1e-3) / 1e9, 1),
+                "side_stream_binning_fwd_bwd_us": round(r_side["ms_per_step"] * 1e3, 1),
             }
-            del s
             torch.cuda.empty_cache()
+        # the earlier schedule at the headline config: binning kernels on a
+        # second stream beside the plain forward kernel
+        print(f"[bench] extra {cfg.name} side-stream binning", file=sys.stderr, flush=True)
+        s = Step(lib, cfg, torch.float32, torch.float32, dev, binning="side")
+        r = time_steps(s, 50, 10)
+        extra[f"{cfg.name}-float32-side-stream-binning"] = {
+            "fwd_bwd_us": round(r["ms_per_step"] * 1e3, 1),
+            "fwd_us": round(r["fwd_ms"] * 1e3, 1),
+            "bin_us": round(r["bin_ms"] * 1e3, 1),
+            "rest_us": round(r["rest_ms"] * 1e3, 1),
+        }
+        del s
+        torch.cuda.empty_cache()
         print("[bench] extra c0 forward", file=sys.stderr, flush=True)
         extra["c0-float32-forward"] = time_forward_only(lib, "c0")
         torch.cuda.empty_cache()

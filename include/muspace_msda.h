@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define MUSPACE_MSDA_ABI_VERSION 4
+#define MUSPACE_MSDA_ABI_VERSION 5
 
 /* the library is built with -fvisibility=hidden; only these symbols export */
 #if defined(__GNUC__)
@@ -167,6 +167,26 @@ MUSPACE_API int ms_deform_attn_backward_rest(
     const void *attention_weights, int geometry_dtype, const void *grad_output,
     float *grad_value, float *grad_sampling_locations, float *grad_attention_weights,
     int64_t batch, int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+/* ms_deform_attn_forward followed by ms_deform_attn_backward_bin on the same
+ * arguments, workspace and stream, in one call: the forward's output plus the
+ * binned workspace (and the parts of the three gradient buffers the binning
+ * writes) that ms_deform_attn_backward_rest then consumes. Where the tile
+ * path applies, the forward kernel itself stores the backward's records
+ * (bin_count and bin_scan run first, over the forward blocks' query chunks),
+ * so the geometry is read once for both and nothing runs beside the forward;
+ * elsewhere it makes exactly those two calls. Same results as the two calls.
+ * No reference counterpart: the reference forward
+ * (/root/reference/csrc/ms_deformable_attn/ms_deform_attn_musa.mu:507-560)
+ * prepares nothing for its backward. */
+MUSPACE_API int ms_deform_attn_forward_bin(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_weights, int geometry_dtype, void *output, float *grad_value,
+    float *grad_sampling_locations, float *grad_attention_weights, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
     int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
     size_t workspace_bytes, void *stream);
 

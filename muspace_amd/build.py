@@ -23,6 +23,7 @@ DEPENDS = (
     PACKAGE_DIR / "csrc" / "msda_device.hpp",
     PACKAGE_DIR / "csrc" / "msda_kernels.hpp",
     PACKAGE_DIR / "csrc" / "msda_backward_tiles.hpp",
+    PACKAGE_DIR / "csrc" / "msda_forward_bin.hpp",
     PACKAGE_DIR / "csrc" / "dfa_kernels.hpp",
     REPO_DIR / "include" / "muspace_msda.h",
     REPO_DIR / "include" / "muspace_dfa.h",

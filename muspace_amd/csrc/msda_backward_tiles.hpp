@@ -67,7 +67,8 @@ constexpr uint32_t kNoItem = 0xffffffffu;
 // Host-computed sizes of the binning scratch (all per (b, m) slab).
 struct BinPlan {
   int chunks;       // query chunks per slab
-  int chunk_q;      // queries per chunk
+  int chunk_q;      // queries per chunk (a power of two)
+  int count_sub;    // chunks counted by one bin_count block (one histogram row each)
   int tile_bound;   // stride of the per-slab tile arrays (>= tiles per slab)
   int lp_log2;      // record id = (position << kPosShift) | (q << lp_log2) | sample
   int rmax;         // records per work item (a multiple of the batch size)
@@ -212,6 +213,9 @@ __device__ __forceinline__ uint32_t block_exclusive(uint32_t run, uint32_t *part
 
 // ------------------------------------------------------------ 1. count ---
 
+// One block per (b, m) slab and group of count_sub consecutive query chunks:
+// a histogram row per chunk (samples per primary tile), written to
+// counts[(slab * chunks + chunk) * tile_bound + tile].
 template <typename GT, int C, int T>
 __global__ void __launch_bounds__(kBinBlock)
     msda_bin_count(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
@@ -220,19 +224,23 @@ __global__ void __launch_bounds__(kBinBlock)
                    float *__restrict__ grad_value) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
-  extern __shared__ uint32_t hist[];
+  extern __shared__ uint32_t hist[];  // [count_sub][nt]
   stage_levels(lv, shapes, starts, s);
   stage_tiles<T>(lv, s.levels, ntc, base);
   const int nt = base[s.levels];
-  for (int i = threadIdx.x; i < nt; i += blockDim.x) hist[i] = 0;
+  const int groups = (p.chunks + p.count_sub - 1) / p.count_sub;
+  const int bm = blockIdx.x / groups, grp = blockIdx.x % groups;
+  const int ch0 = grp * p.count_sub;
+  const int nsub = min(p.count_sub, p.chunks - ch0);
+  for (int i = threadIdx.x; i < nsub * nt; i += blockDim.x) hist[i] = 0;
   // the item counter and the tile kernel's per-XCD take counters
   if (blockIdx.x == 0 && threadIdx.x <= kXcdQueues) item_total[threadIdx.x] = 0;
   __syncthreads();
 
-  const int bm = blockIdx.x / p.chunks, ch = blockIdx.x % p.chunks;
   const int b = bm / s.heads, m = bm % s.heads;
-  const int q0 = ch * p.chunk_q;
-  const int nq = min(p.chunk_q, s.queries - q0);
+  const int q0 = ch0 * p.chunk_q;
+  const int nq = min(nsub * p.chunk_q, s.queries - q0);
+  const int cq_log2 = __builtin_ctz(static_cast<unsigned>(p.chunk_q));
 
   // samples: consecutive threads read consecutive locations of a query; U
   // samples per thread in flight (every load unconditional, clamped index)
@@ -256,23 +264,27 @@ __global__ void __launch_bounds__(kBinBlock)
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * kBinBlock;
       const int l = level_of_sample(live[u] ? smp[u] : 0, s);
       const Tap t = make_tap(lx[u], ly[u], lv[l], live[u]);
-      if (t.in) atomicAdd(&hist[primary_tile<T>(t, ntc[l], base[l])], 1u);
+      const int row = (i >> p.lp_log2) >> cq_log2;  // chunk of the group
+      if (t.in) atomicAdd(&hist[row * nt + primary_tile<T>(t, ntc[l], base[l])], 1u);
     }
   }
 
-  // boundary cells of the slab's tiles ch, ch + chunks, ...
+  // boundary cells of the slab's tiles grp, grp + groups, ...
   const int MC = s.heads * C;
   const size_t slab = static_cast<size_t>(b) * s.spatial * MC + m * C;
-  for (int tl = ch; tl < nt; tl += p.chunks) {
+  for (int tl = grp; tl < nt; tl += groups) {
     const TileGeom g = tile_geom(tl, T, ntc, base);
     zero_tile_cells<C, T>(grad_value, slab, MC, lv[g.l], g, threadIdx.x, blockDim.x,
                           [&](int r, int c) { return boundary_cell(r, c, g); });
   }
   __syncthreads();
-  uint32_t *row = counts + static_cast<size_t>(blockIdx.x) * p.tile_bound;
-  for (int i = threadIdx.x; i < nt; i += blockDim.x) row[i] = hist[i];
+  for (int j = 0; j < nsub; ++j) {
+    uint32_t *row = counts + (static_cast<size_t>(bm) * p.chunks + ch0 + j) * p.tile_bound;
+    for (int i = threadIdx.x; i < nt; i += blockDim.x) row[i] = hist[j * nt + i];
+  }
 }
 
 // ------------------------------------------------------------- 2. scan ---

@@ -20,6 +20,7 @@
 #include "../../include/muspace_msda.h"
 #include "capi_errors.hpp"
 #include "msda_backward_tiles.hpp"
+#include "msda_forward_bin.hpp"
 #include "msda_kernels.hpp"
 
 namespace {
@@ -616,6 +617,25 @@ int tile_grid() {
   return cached[dev];
 }
 
+// The forward row kernel's units (queries of one slab) and tap slots per
+// block: the query chunk of the binning fused into the forward. False where
+// no row kernel serves the channel count.
+bool fwd_bin_chunk(const msda::Shape &s, int value_dtype, int &units, int &slots) {
+  if (s.channels != 16 && s.channels != 32 && s.channels != 64) return false;
+  const int vb = value_dtype == MUSPACE_DTYPE_F32 ? 4 : 2;
+  const int kq = s.channels / (16 / vb);
+  const Launch L = plan_rows(s, kq, vb == 2 && s.channels >= 64 ? 4 : 8, true);
+  const int ng = msda::kWave / kq, gu = 1 << L.plan.gu_log2;
+  const int lchunks = (s.lp + gu * L.ns - 1) / (gu * L.ns);
+  const int waves = msda::kBlock / msda::kWave;
+  units = waves * L.plan.iters * (ng / gu);
+  slots = waves * L.plan.iters * lchunks * ng * L.ns;  // ng * ns <= 64 taps per step
+  return units > 0;
+}
+
+// bin_count blocks per slab: groups of count_sub chunks.
+int count_groups(const msda::BinPlan &p) { return (p.chunks + p.count_sub - 1) / p.count_sub; }
+
 // Scratch layout of the tile-owned backward.
 struct TileWorkspace {
   msda::BinPlan plan;
@@ -633,6 +653,7 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   const int per_q = 4096 >> log2_int(s.lp > 0 ? s.lp : 1);
   p.chunk_q = per_q > msda::kBinBlock ? per_q : msda::kBinBlock;
   p.chunks = (s.queries + p.chunk_q - 1) / p.chunk_q;
+  p.count_sub = 1;
   // a level of n cells has ceil(h/T)*ceil(w/T) <= n/T + 1 tiles
   const int64_t bound = static_cast<int64_t>(s.spatial) / T + s.levels + 1;
   if (bound > msda::kMaxTilesPerSlab) return false;
@@ -685,7 +706,14 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
     off = align256(off + bytes);
     return at;
   };
-  w.counts = take(static_cast<size_t>(bm) * p.chunks * p.tile_bound * 4);
+  // the histograms of either chunking: bin_count's own, or the forward
+  // blocks' when the binning is fused into the forward
+  int fwd_units = 0, fwd_slots = 0;
+  const int fwd_chunks = fwd_bin_chunk(s, value_dtype, fwd_units, fwd_slots)
+                             ? (s.queries + fwd_units - 1) / fwd_units
+                             : 0;
+  const int count_chunks = fwd_chunks > p.chunks ? fwd_chunks : p.chunks;
+  w.counts = take(static_cast<size_t>(bm) * count_chunks * p.tile_bound * 4);
   w.tile_start = take(static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
   w.zero_tiles = take(static_cast<size_t>(bm) * (p.tile_bound + 1) * 4);
   w.records = take(static_cast<size_t>(bm) * p.rec_cap * 16);
@@ -721,7 +749,7 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   const GT *lc = static_cast<const GT *>(loc);
   const GT *aw = static_cast<const GT *>(attn);
   const VT *go = static_cast<const VT *>(grad_out);
-  const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4;
+  const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4 * p.count_sub;
 
   auto count = msda::msda_bin_count<GT, C, T>;
   auto scatter = msda::msda_bin_scatter<GT, C, T>;
@@ -736,8 +764,8 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
                             hipFuncAttributeMaxDynamicSharedMemorySize, tile_bytes);
 
   if (phase != Phase::kRest) {
-    count<<<bm * p.chunks, msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p, counts,
-                                                               item_total, gv);
+    count<<<bm * count_groups(p), msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p,
+                                                                     counts, item_total, gv);
     msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
         shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
     scatter<<<bm * p.chunks, msda::kBinBlock, scatter_bytes, st>>>(
@@ -754,6 +782,94 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
     const int per_slab = static_cast<int>((p.rec_cap + msda::kBinBlock - 1) / msda::kBinBlock);
     msda::msda_grad_gather<<<bm * per_slab, msda::kBinBlock, 0, st>>>(rec_of_sample, records, s,
                                                                       p, per_slab, gl, ga);
+  }
+}
+
+// The forward with the backward's binning fused in (msda_forward_bin.hpp):
+// bin_count and bin_scan over the forward blocks' query chunks, then the
+// forward row kernel, which also stores every chunk's records. Launches
+// nothing and returns false where that does not apply.
+template <typename VT, typename GT, int C>
+bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const int64_t *starts,
+                              const void *loc, const void *attn, void *out, float *gv, float *gl,
+                              float *ga, const msda::Shape &s, const TileWorkspace &w,
+                              void *workspace, hipStream_t st) {
+  constexpr int T = msda::TileCfg<VT, C>::T;
+  constexpr int value_dtype = std::is_same<VT, float>::value ? MUSPACE_DTYPE_F32
+                                                             : MUSPACE_DTYPE_F16;
+  int units = 0, slots = 0;
+  if (!fwd_bin_chunk(s, value_dtype, units, slots)) return false;
+  if (slots > msda::kFwdBinSlots ||
+      msda::fwd_bin_lds_bytes(slots, w.plan.tile_bound) > msda::kFwdBinDynLds) {
+    return false;
+  }
+  unsigned char *ws = static_cast<unsigned char *>(workspace);
+  uint32_t *counts = reinterpret_cast<uint32_t *>(ws + w.counts);
+  uint32_t *tile_start = reinterpret_cast<uint32_t *>(ws + w.tile_start);
+  uint32_t *zero_tiles = reinterpret_cast<uint32_t *>(ws + w.zero_tiles);
+  uint4 *records = reinterpret_cast<uint4 *>(ws + w.records);
+  uint32_t *rec_of_sample = reinterpret_cast<uint32_t *>(ws + w.rec_of_sample);
+  msda::Item *items = reinterpret_cast<msda::Item *>(ws + w.items);
+  uint32_t *item_total = reinterpret_cast<uint32_t *>(ws + w.item_total);
+  msda::BinPlan p = w.plan;
+  p.chunk_q = units;
+  p.chunks = (s.queries + units - 1) / units;
+  // one bin_count block counts about 8192 sample slots (several forward
+  // chunks, a histogram row each), within 64 KB of LDS histograms
+  const int per_chunk = units << p.lp_log2;
+  int sub = per_chunk < 8192 ? 8192 / per_chunk : 1;
+  const int by_lds = 16384 / p.tile_bound;
+  sub = sub < by_lds ? sub : by_lds;
+  p.count_sub = sub > 1 ? sub : 1;
+  const int bm = s.batch * s.heads;
+  const GT *lc = static_cast<const GT *>(loc);
+  const GT *aw = static_cast<const GT *>(attn);
+  const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4 * p.count_sub;
+  auto count = msda::msda_bin_count<GT, C, T>;
+  (void)hipFuncSetAttribute(reinterpret_cast<const void *>(count),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, hist_bytes);
+  count<<<bm * count_groups(p), msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p,
+                                                                   counts, item_total, gv);
+  msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
+      shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
+  const msda::FwdBinArgs args{counts, zero_tiles, records, rec_of_sample, gl, ga, gv, p, slots};
+  const size_t lds = msda::fwd_bin_lds_bytes(slots, p.tile_bound);
+  const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
+  forward_rows_ns<VT, C>(s, [&](auto ns, const Launch &L) {
+    auto k = msda::msda_forward_bin_rows<VT, GT, C, decltype(ns)::value, T>;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    k<<<bm * p.chunks, msda::kBlock, lds, st>>>(static_cast<const VT *>(value), vbytes, shapes,
+                                                 starts, lc, aw, static_cast<VT *>(out), s,
+                                                 L.plan, args);
+  });
+  return true;
+}
+
+template <typename VT, typename GT>
+bool launch_forward_bin(const void *value, const int64_t *shapes, const int64_t *starts,
+                        const void *loc, const void *attn, void *out, float *gv, float *gl,
+                        float *ga, const msda::Shape &s, void *workspace, size_t workspace_bytes,
+                        hipStream_t st) {
+  constexpr int value_dtype = std::is_same<VT, float>::value ? MUSPACE_DTYPE_F32
+                                                             : MUSPACE_DTYPE_F16;
+  TileWorkspace w;
+  const bool fits = plan_tile_workspace(s, value_dtype, w) && workspace != nullptr &&
+                    workspace_bytes >= w.bytes && rows_aligned({value, out, gv}, gl) &&
+                    aligned(workspace, 256);
+  if (!fits) return false;
+  switch (s.channels) {
+    case 16:
+      return launch_forward_bin_tiles<VT, GT, 16>(value, shapes, starts, loc, attn, out, gv, gl,
+                                                  ga, s, w, workspace, st);
+    case 32:
+      return launch_forward_bin_tiles<VT, GT, 32>(value, shapes, starts, loc, attn, out, gv, gl,
+                                                  ga, s, w, workspace, st);
+    case 64:
+      return launch_forward_bin_tiles<VT, GT, 64>(value, shapes, starts, loc, attn, out, gv, gl,
+                                                  ga, s, w, workspace, st);
+    default:
+      return false;
   }
 }
 
@@ -1181,6 +1297,51 @@ int ms_deform_attn_backward_rest(const void *value, int value_dtype,
                        grad_output, grad_value, grad_sampling_locations, grad_attention_weights,
                        a, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
                        Phase::kRest);
+}
+
+int ms_deform_attn_forward_bin(const void *value, int value_dtype, const int64_t *spatial_shapes,
+                               const int64_t *level_start_index, const void *sampling_locations,
+                               const void *attention_weights, int geometry_dtype, void *output,
+                               float *grad_value, float *grad_sampling_locations,
+                               float *grad_attention_weights, int64_t batch,
+                               int64_t spatial_size, int64_t num_heads, int64_t channels,
+                               int64_t num_levels, int64_t num_query, int64_t num_point,
+                               int64_t im2col_step, void *workspace, size_t workspace_bytes,
+                               void *stream) {
+  static const char *fn = "ms_deform_attn_forward_bin";
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  msda::Shape s;
+  if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  bool fused = false;
+  if (needs_data(s) && s.lp > 0) {
+    if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+        !attention_weights || !output || !grad_value || !grad_sampling_locations ||
+        !grad_attention_weights) {
+      return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+    }
+    with_dtypes(value_dtype, geometry_dtype, [&](auto vt, auto gt) {
+      fused = launch_forward_bin<decltype(vt), decltype(gt)>(
+          value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+          output, grad_value, grad_sampling_locations, grad_attention_weights, s, workspace,
+          workspace_bytes, st);
+    });
+    if (fused) return check_launch(fn);
+  }
+  // the two calls this one stands for
+  if (int rc = ms_deform_attn_forward(value, value_dtype, spatial_shapes, level_start_index,
+                                      sampling_locations, attention_weights, geometry_dtype,
+                                      output, batch, spatial_size, num_heads, channels,
+                                      num_levels, num_query, num_point, im2col_step, stream)) {
+    return rc;
+  }
+  return ms_deform_attn_backward_bin(value, value_dtype, spatial_shapes, level_start_index,
+                                     sampling_locations, attention_weights, geometry_dtype,
+                                     nullptr, grad_value, grad_sampling_locations,
+                                     grad_attention_weights, batch, spatial_size, num_heads,
+                                     channels, num_levels, num_query, num_point, im2col_step,
+                                     workspace, workspace_bytes, stream);
 }
 
 int ms_deform_attn_backward(const void *value, int value_dtype, const int64_t *spatial_shapes,

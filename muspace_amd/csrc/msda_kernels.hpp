@@ -233,6 +233,24 @@ struct CameraSlots {
   }
 };
 
+// Hooks of forward_rows that also fix a block's units. NoBin: blocks of
+// per_block consecutive units (in the order u = (b*M + m)*nq + q), no
+// binning. A binning hook (TileBinner, msda_backward_tiles.hpp) sees each live
+// sample's tap as the forward computes it.
+struct NoBin {
+  static constexpr bool kActive = false;
+  __device__ __forceinline__ int64_t first_unit(int lb, int64_t per_block, const Shape &) const {
+    return static_cast<int64_t>(lb) * per_block;
+  }
+  __device__ __forceinline__ int64_t end_unit(int, int64_t, const Shape &s) const {
+    return s.units;
+  }
+  __device__ __forceinline__ void begin(const Level *, const Shape &) {}
+  __device__ __forceinline__ void sample(const Tap &, int, int, int, float, bool, int,
+                                         const Shape &) {}
+  __device__ __forceinline__ void finish(const Shape &) {}
+};
+
 // Forward row kernel. Per step (a chunk of NS samples for each lane group),
 // lane i < NG*NS computes one sample's bilinear tap -- the four corner byte
 // offsets (kOobOffset for a corner outside the level) and the four weights
@@ -263,13 +281,15 @@ struct CameraSlots {
 // step (the common case, L*P <= GU*NS) that is the plain exp(x - max) / sum.
 // The reductions are branch-free (every step computed, uniform selects), so
 // they schedule with the tap's own arithmetic.
-template <typename VT, typename GT, int C, int NS, typename Out, bool kSoftmax = false>
+template <typename VT, typename GT, int C, int NS, typename Out, bool kSoftmax = false,
+          typename Bin = NoBin>
 __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint32_t value_bytes,
                                              const int64_t *__restrict__ shapes,
                                              const int64_t *__restrict__ starts,
                                              const GT *__restrict__ loc,
                                              const GT *__restrict__ attn, const Out &out,
-                                             const Shape &s, const RowPlan &plan, int lb) {
+                                             const Shape &s, const RowPlan &plan, int lb,
+                                             Bin &bin) {
   constexpr int CPL = RowTraits<VT>::kCpl;
   constexpr int VB = static_cast<int>(sizeof(VT));
   constexpr int KQ = C / CPL;
@@ -294,6 +314,7 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   // kSoftmax, per step parity and unit slot: the step's rescale and 1/sum
   __shared__ float2 unit_norm[2][kSoftmax ? kBlock : 1];
   stage_levels(lv, shapes, starts, s);
+  bin.begin(lv, s);
   const __amdgpu_buffer_rsrc_t vr = make_rsrc(value, value_bytes);
 
   const int lane = threadIdx.x % kWave;
@@ -311,13 +332,17 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   const int my_entry = wave * TW + tg * (NS + PAD) + tj;
   const int grp_entry = wave * TW + grp * (NS + PAD);
 
-  const int64_t wave_id = static_cast<int64_t>(lb) * (kBlock / kWave) + wave;
   const int chunks = (s.lp + GU * NS - 1) / (GU * NS);
   const int steps = plan.iters * chunks;
 
   // geometry of this lane's tap sample in step st; the tap unit and the
-  // output unit advance by UW units per wave iteration
-  const int64_t u_first = wave_id * plan.iters * UW;
+  // output unit advance by UW units per wave iteration. The block's units
+  // are [first_unit, end_unit) (the hook object decides; NoBin: blocks of
+  // per_block consecutive units up to s.units)
+  const int64_t per_block = static_cast<int64_t>(kBlock / kWave) * plan.iters * UW;
+  const int64_t u_first = bin.first_unit(lb, per_block, s) +
+                          static_cast<int64_t>(wave) * plan.iters * UW;
+  const int64_t u_end = bin.end_unit(lb, per_block, s);
   UnitIter tu, ou, on;  // on: the output unit after ou
   tu.init(u_first + tslot, s);
   ou.init(u_first + slot, s);
@@ -359,7 +384,7 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
     const int it = st / chunks, s0 = (st % chunks) * GU * NS;
     if (st > 0 && st % chunks == 0) tu.advance(UW, s);
     const int64_t u64 = u_first + static_cast<int64_t>(it) * UW + tslot;
-    const bool live = st < steps && u64 < s.units && lane < NG * NS;
+    const bool live = st < steps && u64 < u_end && lane < NG * NS;
     const int smp = s0 + tgi + GU * tj;
     ok = live && smp < s.lp;
     sm = ok ? smp : 0;
@@ -374,8 +399,14 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   };
   // A. this lane's tap of step st (geometry loaded) into table st & 1
   auto tap = [&](int st) {
-    const Level L = lv[level_of_sample(sm, s)];
+    const int l = level_of_sample(sm, s);
+    const Level L = lv[l];
     const Tap t = make_tap(lx, ly, L, ok);
+    // the binning hook sees every live sample once: slot = its place in the
+    // block's tap order (st < steps whenever ok)
+    if constexpr (Bin::kActive) {
+      bin.sample(t, l, tu.q, sm, ok ? a : 0.0f, ok, (wave * steps + st) * (NG * NS) + lane, s);
+    }
     float ai = ok ? a : 0.0f;
     if constexpr (kSoftmax) {
       softmax_step(st);
@@ -456,7 +487,7 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
       for (int j = 0; j < CPL; ++j) acc[j] *= inv;
     }
     const int64_t u64 = u_first + static_cast<int64_t>(st / chunks) * UW + slot;
-    if (u64 < s.units && gi == 0) {
+    if (u64 < u_end && gi == 0) {
       out.template put<C, CPL>(ou.b, ou.q, ou.m, k, acc, tk_cur, s);
     }
     if constexpr (Out::kLoadsAhead) {
@@ -503,6 +534,7 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
       end_step(st);
     }
   }
+  bin.finish(s);
 }
 
 template <typename VT, typename GT, int C, int NS>
@@ -511,8 +543,9 @@ __global__ void __launch_bounds__(kBlock)
                       const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                       const GT *__restrict__ loc, const GT *__restrict__ attn,
                       VT *__restrict__ out, Shape s, RowPlan plan) {
+  NoBin nb;
   forward_rows<VT, GT, C, NS>(value, value_bytes, shapes, starts, loc, attn, DenseRows<VT>{out},
-                              s, plan, xcd_logical_block(blockIdx.x, gridDim.x));
+                              s, plan, xcd_logical_block(blockIdx.x, gridDim.x), nb);
 }
 
 // Forward with the attention weights given as logits: softmax over each
@@ -524,9 +557,10 @@ __global__ void __launch_bounds__(kBlock)
                               const int64_t *__restrict__ starts, const GT *__restrict__ loc,
                               const GT *__restrict__ logits, VT *__restrict__ out, Shape s,
                               RowPlan plan) {
+  NoBin nb;
   forward_rows<VT, GT, C, NS, DenseRows<VT>, true>(value, value_bytes, shapes, starts, loc,
                                                    logits, DenseRows<VT>{out}, s, plan,
-                                                   xcd_logical_block(blockIdx.x, gridDim.x));
+                                                   xcd_logical_block(blockIdx.x, gridDim.x), nb);
 }
 
 // Cameras of the spatial cross-attention, summed into the BEV slots
@@ -542,7 +576,8 @@ __global__ void __launch_bounds__(kBlock)
   int lb = xcd_logical_block(blockIdx.x, gridDim.x);
   Shape sc = s;
   const CameraSlots<VT, GT, kAtomic> cam = out.segment(lb, sc);
-  forward_rows<VT, GT, C, NS>(value, value_bytes, shapes, starts, loc, attn, cam, sc, plan, lb);
+  NoBin nb;
+  forward_rows<VT, GT, C, NS>(value, value_bytes, shapes, starts, loc, attn, cam, sc, plan, lb, nb);
 }
 
 // ------------------------------------------------------------ backward ---

@@ -133,13 +133,17 @@ def _native_geometry_dtype(value: torch.Tensor, *geometry: torch.Tensor) -> torc
 
 
 # Early binning: the tile-owned backward's binning reads only the geometry, so
-# the forward starts it on a second stream where it overlaps the forward
-# kernel (c2 step 1255 -> 1204 us measured). The backward's buffers (its
-# scratch and the three float32 gradients) then live from the forward to the
+# the forward does it. ms_deform_attn_forward_bin runs the forward and the
+# binning as one call, in which the forward kernel itself stores the
+# backward's records (the geometry is read once for both; a binning on a second
+# stream beside the forward kernel could not overlap it, the forward's
+# registers leaving no room on its SIMDs). The backward's buffers (its scratch
+# and the three float32 gradients) then live from the forward to the
 # backward; MUSPACE_EARLY_BINNING=0 turns this off, and a per-device byte
 # budget bounds what all forwards awaiting their backward may hold
 # (MUSPACE_EARLY_BINNING_BUDGET bytes, default 1/32 of the device's memory):
-# a forward that would exceed it does not bin early.
+# a forward that would exceed it does not bin early. The softmax operator
+# (msda_softmax.py) still bins on a second stream.
 EARLY_BINNING_ENV = "MUSPACE_EARLY_BINNING"
 EARLY_BINNING_BUDGET_ENV = "MUSPACE_EARLY_BINNING_BUDGET"
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
@@ -225,10 +229,9 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return stream
 
 
-def _start_binning(ext, value, spatial, starts, sampling, attn, im2col_step):
-    """Allocate the backward's workspace and gradients and run its binning on a
-    side stream, ordered after the work that produced the inputs. Returns the
-    buffers and the completion event, or None when the shape takes the atomic
+def _binning_buffers(ext, value, sampling, attn):
+    """The backward's workspace and float32 gradients, allocated in the
+    forward for a binning there; None when the shape takes the atomic
     backward (nothing to bin) or the early-binning budget is spent."""
     nbytes = ext.backward_workspace_bytes(value, sampling)
     if nbytes <= 1:
@@ -244,18 +247,7 @@ def _start_binning(ext, value, spatial, starts, sampling, attn, im2col_step):
         torch.empty(sampling.shape, dtype=torch.float32, device=device),
         torch.empty(attn.shape, dtype=torch.float32, device=device),
     )
-    main = torch.cuda.current_stream(device)
-    side = _side_stream(device)
-    ready = torch.cuda.Event()
-    ready.record(main)
-    side.wait_event(ready)
-    ext.ms_deform_attn_backward_bin(value, spatial, starts, sampling, attn, *grads, im2col_step,
-                                    workspace, stream=side)
-    for tensor in (workspace, *grads, value, spatial, starts, sampling, attn):
-        tensor.record_stream(side)
-    done = torch.cuda.Event()
-    done.record(side)
-    return workspace, grads, done
+    return workspace, grads
 
 
 class _NativeMSDAFunction(torch.autograd.Function):
@@ -286,16 +278,19 @@ class _NativeMSDAFunction(torch.autograd.Function):
         output = value_arg.new_empty(
             (value_arg.size(0), sampling_arg.size(1), value_arg.size(2) * value_arg.size(3))
         )
-        # every tensor is checked before the first launch (the binning below
-        # runs before the forward's own launch)
+        # every tensor is checked before anything is allocated or launched
         ext.check_forward(value_arg, spatial_arg, start_arg, sampling_arg, attn_arg, output)
         ctx.binned = None
         if early_binning and any(ctx.needs_input_grad[i] for i in (0, 3, 4)):
-            ctx.binned = _start_binning(ext, value_arg, spatial_arg, start_arg, sampling_arg,
-                                        attn_arg, im2col_step)
-        ext.ms_deform_attn_forward(
-            value_arg, spatial_arg, start_arg, sampling_arg, attn_arg, output, im2col_step
-        )
+            ctx.binned = _binning_buffers(ext, value_arg, sampling_arg, attn_arg)
+        if ctx.binned is not None:
+            workspace, grads = ctx.binned
+            ext.ms_deform_attn_forward_bin(value_arg, spatial_arg, start_arg, sampling_arg,
+                                           attn_arg, output, *grads, im2col_step, workspace)
+        else:
+            ext.ms_deform_attn_forward(
+                value_arg, spatial_arg, start_arg, sampling_arg, attn_arg, output, im2col_step
+            )
         ctx.save_for_backward(value_arg, spatial_arg, start_arg, sampling_arg, attn_arg)
         return output
 
@@ -310,8 +305,9 @@ class _NativeMSDAFunction(torch.autograd.Function):
         grad = grad_output.to(value.dtype).contiguous()
         binned, ctx.binned = ctx.binned, None  # one backward per binning
         if binned is not None:
-            workspace, (grad_value, grad_sampling, grad_attention), done = binned
-            torch.cuda.current_stream(value.device).wait_event(done)
+            # the binning ran in the forward's call, on the stream autograd
+            # runs this backward on
+            workspace, (grad_value, grad_sampling, grad_attention) = binned
             ext.ms_deform_attn_backward_rest(
                 value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
                 grad, grad_value, grad_sampling, grad_attention, ctx.im2col_step, workspace,

@@ -25,7 +25,7 @@ from pathlib import Path
 from typing import Any, Callable
 
 LIBRARY_RELPATH = "native/libmuspace_msda.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
@@ -70,6 +70,12 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         + [_c_ptr, ctypes.c_size_t, _c_ptr],
     ),
     "ms_deform_attn_backward_rest": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "ms_deform_attn_forward_bin": (
         _c_int,
         [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
         + [_c_int64] * 8
@@ -204,6 +210,7 @@ class NativeLibrary:
             "backward_softmax_workspace_bytes": self.backward_softmax_workspace_bytes,
             "ms_deform_attn_backward_bin": self.ms_deform_attn_backward_bin,
             "ms_deform_attn_backward_rest": self.ms_deform_attn_backward_rest,
+            "ms_deform_attn_forward_bin": self.ms_deform_attn_forward_bin,
             "ms_deform_attn_forward_softmax": self.ms_deform_attn_forward_softmax,
             "ms_deform_attn_backward_softmax": self.ms_deform_attn_backward_softmax,
             "backward_softmax_workspace": self.backward_softmax_workspace,
@@ -533,6 +540,42 @@ class NativeLibrary:
                          level_start_index, sampling_locations, attention_weights, grad_output,
                          grad_value, grad_sampling_locations, grad_attention_weights,
                          im2col_step, workspace, None)
+
+    def ms_deform_attn_forward_bin(
+        self, value, spatial_shapes, level_start_index, sampling_locations, attention_weights,
+        output, grad_value, grad_sampling_locations, grad_attention_weights, im2col_step,
+        workspace,
+    ) -> None:
+        """The forward and the first part of the backward (binning) in one call
+        on the current stream: writes ``output`` and bins into ``workspace``,
+        as :meth:`ms_deform_attn_forward` followed by
+        :meth:`ms_deform_attn_backward_bin` would. Where the tile path applies
+        the forward kernel stores the backward's records itself. Every tensor
+        is checked before the first launch;
+        :meth:`ms_deform_attn_backward_rest` on the same workspace and
+        gradients must follow it on a stream ordered after this one."""
+        import torch
+
+        self.check_forward(value, spatial_shapes, level_start_index, sampling_locations,
+                           attention_weights, output)
+        self._check_split(value, spatial_shapes, level_start_index, sampling_locations,
+                          attention_weights, None, grad_value, grad_sampling_locations,
+                          grad_attention_weights, workspace, False)
+        batch, spatial, heads, channels = value.shape
+        levels = spatial_shapes.shape[0]
+        queries, points = sampling_locations.shape[1], sampling_locations.shape[4]
+        name = "ms_deform_attn_forward_bin"
+        with torch.cuda.device(value.device):
+            rc = self._raw[name](
+                value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),
+                level_start_index.data_ptr(), sampling_locations.data_ptr(),
+                attention_weights.data_ptr(), _dtype_code(sampling_locations.dtype),
+                output.data_ptr(), grad_value.data_ptr(), grad_sampling_locations.data_ptr(),
+                grad_attention_weights.data_ptr(), batch, spatial, heads, channels, levels,
+                queries, points, int(im2col_step), workspace.data_ptr(), workspace.numel(),
+                self._stream(value),
+            )
+        self._raise_on(rc, name)
 
     def ms_deform_attn_backward_softmax_bin(
         self, value, spatial_shapes, level_start_index, sampling_locations, attention_logits,

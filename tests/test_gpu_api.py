@@ -192,9 +192,10 @@ def test_autograd_end_to_end_fp32_full_channel_layout():
 
 
 def test_early_binning_matches_the_one_call_backward(monkeypatch):
-    """The autograd function bins on a side stream during the forward; the
-    result equals the one-call backward (MUSPACE_EARLY_BINNING=0), and a
-    second backward (retain_graph) takes the one-call path."""
+    """The autograd function bins in its forward call (the forward kernel
+    stores the backward's records); the result equals the one-call backward
+    (MUSPACE_EARLY_BINNING=0), and a second backward (retain_graph) takes the
+    one-call path."""
     def grads(early):
         monkeypatch.setenv("MUSPACE_EARLY_BINNING", "1" if early else "0")
         value, shapes, starts, loc, attn = _fixture(device=DEV, batch=2, queries=300, heads=8,
@@ -231,8 +232,7 @@ def test_no_binning_when_no_graph_is_recorded(monkeypatch):
     assert [name for name, _ in spy.calls] == ["ms_deform_attn_forward"]
     spy.calls.clear()
     multi_scale_deformable_attn(*tensors, backend="hip")
-    assert [name for name, _ in spy.calls] == ["ms_deform_attn_backward_bin",
-                                               "ms_deform_attn_forward"]
+    assert [name for name, _ in spy.calls] == ["ms_deform_attn_forward_bin"]
 
 
 @pytest.mark.parametrize("embed_dims", [32, 3])

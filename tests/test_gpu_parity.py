@@ -66,6 +66,29 @@ def run_backward(lib, t, grad, value_dtype, geometry_dtype, im2col_step=64):
     return gv, gl, ga
 
 
+def run_fused(lib, t, grad, value_dtype, geometry_dtype, im2col_step=64):
+    """ms_deform_attn_forward_bin (the forward kernel stores the backward's
+    records), then ms_deform_attn_backward_rest: output and gradients."""
+    value = t["value"].to(value_dtype).to(DEV).contiguous()
+    loc = t["sampling_locations"].to(geometry_dtype).to(DEV).contiguous()
+    attn = t["attention_weights"].to(geometry_dtype).to(DEV).contiguous()
+    shapes, starts = t["spatial_shapes"].to(DEV), t["level_start_index"].to(DEV)
+    # poisoned: every element of the output and all three gradients must be
+    # overwritten
+    out = torch.full((value.shape[0], loc.shape[1], value.shape[2] * value.shape[3]),
+                     float("nan"), dtype=value_dtype, device=DEV)
+    gv = torch.full(value.shape, float("nan"), dtype=torch.float32, device=DEV)
+    gl = torch.full(loc.shape, float("nan"), dtype=torch.float32, device=DEV)
+    ga = torch.full(attn.shape, float("nan"), dtype=torch.float32, device=DEV)
+    ws = lib.backward_workspace(value, loc)
+    lib.ms_deform_attn_forward_bin(value, shapes, starts, loc, attn, out, gv, gl, ga,
+                                   im2col_step, ws)
+    lib.ms_deform_attn_backward_rest(value, shapes, starts, loc, attn,
+                                     grad.to(value_dtype).to(DEV).contiguous(), gv, gl, ga,
+                                     im2col_step, ws)
+    return out, gv, gl, ga
+
+
 def oracle_inputs(t, value_dtype, geometry_dtype):
     """The oracle sees exactly what the kernel reads, upcast to float32."""
     return (
@@ -179,6 +202,67 @@ def test_binning_chunk_boundaries_match_oracle(native_lib, case, dtypes):
     _assert_close(gv, o_gv, btol, "grad_value")
     _assert_close(gl, o_gl, btol, "grad_sampling_locations")
     _assert_close(ga, o_ga, btol, "grad_attention_weights")
+
+
+# The fused forward + binning (ms_deform_attn_forward_bin, then _rest) on
+# small and medium shapes against the full oracle: every row-kernel channel
+# count, ragged last forward chunks (L*P = 3: 64-query chunks, 1000 = 15 x 64
+# + 40), one chunk shorter than a block, samples outside their level (zero
+# gradients written by the forward), a single dense tile split into several
+# work items (3 x 4 level, 24000 records per slab), and 16-bit values with
+# float32 or 16-bit geometry.
+FUSED = [
+    (2, 23, 8, 32, ((17, 11),), 4),
+    (3, 17, 8, 32, ((8, 9), (4, 5)), 4),
+    (2, 9, 8, 32, ((10, 12), (5, 6), (3, 3), (2, 2)), 8),
+    (1, 5, 2, 32, ((10, 12), (5, 6), (3, 3), (2, 2)), 16),
+    (2, 21, 8, 16, ((9, 10), (4, 5)), 4),
+    (2, 21, 4, 64, ((9, 10), (4, 5)), 4),
+    (1, 1000, 2, 32, ((20, 30), (10, 15), (5, 8)), 1),
+    (1, 300, 8, 32, ((20, 30), (10, 15), (5, 8), (3, 4)), 8),
+    (2, 3000, 1, 32, ((3, 4),), 8),
+    (1, 1100, 2, 16, ((12, 18), (6, 9), (3, 5)), 2),
+    (1, 1100, 2, 64, ((12, 18), (6, 9), (3, 5)), 2),
+]
+
+
+@pytest.mark.parametrize("dtypes", DTYPES, ids=lambda d: f"{d[0]}-{d[1]}".replace("torch.", ""))
+@pytest.mark.parametrize("case", FUSED, ids=_id)
+def test_fused_forward_binning_matches_oracle(native_lib, case, dtypes):
+    value_dtype, geometry_dtype = dtypes
+    print(f"[parity] fused {_id(case)} {value_dtype}/{geometry_dtype}", flush=True)
+    t, grad = small_case(sum(case[:4]), *case)
+    out, gv, gl, ga = run_fused(native_lib, t, grad, value_dtype, geometry_dtype)
+    plain = run_forward(native_lib, t, value_dtype, geometry_dtype)
+    torch.cuda.synchronize()
+    o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
+        *oracle_inputs(t, value_dtype, geometry_dtype), grad.to(value_dtype).float()
+    )
+    ftol, btol = TOL[value_dtype]
+    _assert_close(out, plain, 1e-6, "output against the plain forward")
+    _assert_close(out, o_out, ftol, "output")
+    _assert_close(gv, o_gv, btol, "grad_value")
+    _assert_close(gl, o_gl, btol, "grad_sampling_locations")
+    _assert_close(ga, o_ga, btol, "grad_attention_weights")
+
+
+def test_fused_forward_binning_records_path_matches_oracle(native_lib):
+    """A slab span of queries x L*P x 12 bytes above 4 MB: the tile kernel
+    stores the location and weight gradients over the records and
+    msda_grad_gather copies them into sample order through the
+    sample -> record index that the fused forward wrote."""
+    case = (1, 11000, 2, 32, ((20, 30),), 32)
+    print(f"[parity] fused records path {_id(case)}", flush=True)
+    t, grad = small_case(91, *case)
+    out, gv, gl, ga = run_fused(native_lib, t, grad, torch.float32, torch.float32)
+    torch.cuda.synchronize()
+    o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
+        *oracle_inputs(t, torch.float32, torch.float32), grad
+    )
+    _assert_close(out, o_out, 1e-5, "output")
+    _assert_close(gv, o_gv, 1e-4, "grad_value")
+    _assert_close(gl, o_gl, 1e-4, "grad_sampling_locations")
+    _assert_close(ga, o_ga, 1e-4, "grad_attention_weights")
 
 
 def test_im2col_step_chunking_has_no_numeric_effect(native_lib):
@@ -296,18 +380,48 @@ SUBSET = 48  # queries per config checked against the oracle
 @pytest.mark.parametrize("name,value_dtype,geometry_dtype", FULL,
                          ids=[f"{n}-{str(v).replace('torch.', '')}" for n, v, _ in FULL])
 def test_full_config_parity(native_lib, name, value_dtype, geometry_dtype):
+    _check_full_config(native_lib, name, value_dtype, geometry_dtype, fused=False)
+
+
+# The fused forward + binning at full size: the direct gradient writes (c2,
+# c3), the records-plus-gather path (c1, c4) and 16-bit values (c4).
+FULL_FUSED = [
+    ("c1", torch.float32, torch.float32),
+    ("c2", torch.float32, torch.float32),
+    ("c3", torch.float32, torch.float32),
+    ("c4", torch.bfloat16, torch.float32),
+]
+
+
+@pytest.mark.parametrize("name,value_dtype,geometry_dtype", FULL_FUSED,
+                         ids=[f"{n}-{str(v).replace('torch.', '')}" for n, v, _ in FULL_FUSED])
+def test_full_config_parity_fused_binning(native_lib, name, value_dtype, geometry_dtype):
+    _check_full_config(native_lib, name, value_dtype, geometry_dtype, fused=True)
+
+
+def _check_full_config(native_lib, name, value_dtype, geometry_dtype, fused):
     cfg = CONFIGS[name]
-    print(f"[parity] {name} {value_dtype} bs={cfg.batch} nq={cfg.queries}", flush=True)
+    print(f"[parity] {name} {value_dtype} bs={cfg.batch} nq={cfg.queries} fused={fused}",
+          flush=True)
     t = make_inputs(cfg, value_dtype=torch.float32)
     grad = t.pop("grad_output")
-    out = run_forward(native_lib, t, value_dtype, geometry_dtype)
-    gv, gl, ga = run_backward(native_lib, t, grad, value_dtype, geometry_dtype)
+    if fused:
+        out, gv, gl, ga = run_fused(native_lib, t, grad, value_dtype, geometry_dtype)
+        plain = run_forward(native_lib, t, value_dtype, geometry_dtype)
+        torch.cuda.synchronize()
+        _assert_close(out, plain, 1e-6, "output against the plain forward")
+    else:
+        out = run_forward(native_lib, t, value_dtype, geometry_dtype)
+        gv, gl, ga = run_backward(native_lib, t, grad, value_dtype, geometry_dtype)
     g = torch.Generator().manual_seed(7)
     idx = torch.randperm(cfg.queries, generator=g)[:SUBSET].sort().values
     mask = torch.zeros(cfg.queries, dtype=torch.bool)
     mask[idx] = True
     grad_masked = grad * mask.view(1, -1, 1)
-    gv_sub, _, _ = run_backward(native_lib, t, grad_masked, value_dtype, geometry_dtype)
+    if fused:
+        _, gv_sub, _, _ = run_fused(native_lib, t, grad_masked, value_dtype, geometry_dtype)
+    else:
+        gv_sub, _, _ = run_backward(native_lib, t, grad_masked, value_dtype, geometry_dtype)
     torch.cuda.synchronize()
 
     value, shapes, loc, attn = oracle_inputs(t, value_dtype, geometry_dtype)

@@ -97,7 +97,12 @@ def recording(monkeypatch, native_lib):
         ext_.calls.append("ms_deform_attn_backward_bin")
         return None
 
-    monkeypatch.setattr(msda_module, "_start_binning", bins)
+    def buffers(ext_, value, loc, attn):  # host stand-ins for the device buffers
+        ext_.calls.append("backward_workspace")
+        return (torch.empty(1 << 12, dtype=torch.uint8),
+                (torch.empty(value.shape), torch.empty(loc.shape), torch.empty(attn.shape)))
+
+    monkeypatch.setattr(msda_module, "_binning_buffers", buffers)
     monkeypatch.setattr(softmax_module, "_start_binning", bins)
     monkeypatch.setenv("MUSPACE_EARLY_BINNING", "1")
     return ext
@@ -108,7 +113,7 @@ def test_valid_inputs_are_checked_then_binned_then_run(recording):
     out = msda_module.multi_scale_deformable_attn(*_inputs(), backend="auto")
     assert out.shape == (BATCH, QUERIES, HEADS * CHANNELS)
     assert recording.calls == ["check_forward", "backward_workspace",
-                               "ms_deform_attn_backward_bin", "ms_deform_attn_forward"]
+                               "ms_deform_attn_forward_bin"]
     assert get_last_dispatch_report().selected_backend == "hip"
 
 
@@ -206,6 +211,20 @@ def test_binning_entry_checks_its_own_arguments(native_lib, raw_launches, part, 
     with pytest.raises(RuntimeError, match=message):
         getattr(native_lib, part)(value, shapes, starts, loc, attn, *_grads(value, loc, attn),
                                   64, workspace, stream=object())
+    assert raw_launches == []
+
+
+@pytest.mark.parametrize("case", sorted(BAD))
+def test_fused_forward_binning_entry_checks_its_own_arguments(native_lib, raw_launches, case):
+    spoil, message = BAD[case]
+    tensors = [t.detach() if t.dtype.is_floating_point else t for t in _inputs(False)]
+    spoil(tensors)
+    value, shapes, starts, loc, attn = tensors
+    out = torch.empty(BATCH, QUERIES, HEADS * CHANNELS)
+    workspace = torch.empty(1 << 20, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match=message):
+        native_lib.ms_deform_attn_forward_bin(value, shapes, starts, loc, attn, out,
+                                              *_grads(value, loc, attn), 64, workspace)
     assert raw_launches == []
 
 
