@@ -797,6 +797,12 @@ bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const in
   constexpr int T = msda::TileCfg<VT, C>::T;
   constexpr int value_dtype = std::is_same<VT, float>::value ? MUSPACE_DTYPE_F32
                                                              : MUSPACE_DTYPE_F16;
+  // Only where the tile kernel writes the location and weight gradients
+  // straight to sample order: with the records-plus-gather path (c1, c4)
+  // the fused forward also stores the sample -> record index, and at c4
+  // its LDS leaves two blocks per CU where the 16-bit forward keeps three
+  // (fused c4 bf16 step 2969 against 2953 us with the binning kernels).
+  if (!w.plan.direct) return false;
   int units = 0, slots = 0;
   if (!fwd_bin_chunk(s, value_dtype, units, slots)) return false;
   if (slots > msda::kFwdBinSlots ||
@@ -808,20 +814,24 @@ bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const in
   uint32_t *tile_start = reinterpret_cast<uint32_t *>(ws + w.tile_start);
   uint32_t *zero_tiles = reinterpret_cast<uint32_t *>(ws + w.zero_tiles);
   uint4 *records = reinterpret_cast<uint4 *>(ws + w.records);
-  uint32_t *rec_of_sample = reinterpret_cast<uint32_t *>(ws + w.rec_of_sample);
   msda::Item *items = reinterpret_cast<msda::Item *>(ws + w.items);
   uint32_t *item_total = reinterpret_cast<uint32_t *>(ws + w.item_total);
   msda::BinPlan p = w.plan;
+  const int bm = s.batch * s.heads;
   p.chunk_q = units;
   p.chunks = (s.queries + units - 1) / units;
-  // one bin_count block counts about 8192 sample slots (several forward
-  // chunks, a histogram row each), within 64 KB of LDS histograms
+  // bin_count blocks count several forward chunks each (a histogram row per
+  // chunk) when there would be more than about 4096 blocks, up to 8192
+  // sample slots and 64 KB of LDS histograms per block: its cost per block
+  // (level tables, histogram clear and flush) dominated at c4 (22560 chunks;
+  // count and scan 250 -> 166 us), while at c2 (7536 chunks) four per block
+  // left too few blocks (42 -> 60 us)
   const int per_chunk = units << p.lp_log2;
-  int sub = per_chunk < 8192 ? 8192 / per_chunk : 1;
-  const int by_lds = 16384 / p.tile_bound;
+  int sub = bm * p.chunks / 4096;
+  const int by_slots = 8192 / per_chunk, by_lds = 16384 / p.tile_bound;
+  sub = sub < by_slots ? sub : by_slots;
   sub = sub < by_lds ? sub : by_lds;
   p.count_sub = sub > 1 ? sub : 1;
-  const int bm = s.batch * s.heads;
   const GT *lc = static_cast<const GT *>(loc);
   const GT *aw = static_cast<const GT *>(attn);
   const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4 * p.count_sub;
@@ -832,7 +842,7 @@ bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const in
                                                                    counts, item_total, gv);
   msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
       shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
-  const msda::FwdBinArgs args{counts, zero_tiles, records, rec_of_sample, gl, ga, gv, p, slots};
+  const msda::FwdBinArgs args{counts, zero_tiles, records, gl, ga, gv, p, slots};
   const size_t lds = msda::fwd_bin_lds_bytes(slots, p.tile_bound);
   const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
   forward_rows_ns<VT, C>(s, [&](auto ns, const Launch &L) {

@@ -195,6 +195,26 @@ __device__ __forceinline__ void store16_nt(T *p, const float (&v)[8]) {
   __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (ctrl), 0xF, 0xF, \
                                              false))
 
+// Inclusive prefix sum over the 64 lanes of a wavefront, all in DPP: a
+// Kogge-Stone scan inside each 16-lane row (row_shr 1, 2, 4, 8; lanes
+// shifted in from outside the row read 0), then row 0's total added to rows
+// 1 and 3 and row 1's running total to rows 2 and 3 (row_bcast 15 and 31, a
+// row mask picking the rows that receive it). Six VALU instructions instead
+// of six LDS-routed shuffles. Must be called with the whole wavefront active.
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+#define MSDA_DPP_U32(x, ctrl, rows)                                                      \
+  static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), (ctrl), (rows), \
+                                                    0xF, true))
+  v += MSDA_DPP_U32(v, 0x111, 0xF);  // row_shr:1
+  v += MSDA_DPP_U32(v, 0x112, 0xF);  // row_shr:2
+  v += MSDA_DPP_U32(v, 0x114, 0xF);  // row_shr:4
+  v += MSDA_DPP_U32(v, 0x118, 0xF);  // row_shr:8
+  v += MSDA_DPP_U32(v, 0x142, 0xA);  // row_bcast:15 -> rows 1, 3
+  v += MSDA_DPP_U32(v, 0x143, 0xC);  // row_bcast:31 -> rows 2, 3
+#undef MSDA_DPP_U32
+  return v;
+}
+
 // Sum over aligned groups of N consecutive lanes (N a power of two <= 64);
 // every lane of the group receives the total. Must be called with the whole
 // wavefront active.

@@ -25,7 +25,10 @@
 // us, c4 bf16 1791 against 1510 us.
 //
 // The records, tile ranges and work items are those of the three-kernel
-// binning, so msda_tile_backward runs on them unchanged.
+// binning, so msda_tile_backward runs on them unchanged. The host takes this
+// path only where the tile kernel writes the location and weight gradients
+// straight to sample order (BinPlan::direct), so no sample -> record index
+// is written here.
 #pragma once
 
 #include "msda_backward_tiles.hpp"
@@ -53,7 +56,6 @@ struct FwdBinArgs {
   const uint32_t *cursors;     // bin_scan's per-(chunk, tile) record cursors
   const uint32_t *zero_tiles;  // per slab {count, tile...}: empty and split tiles
   uint4 *records;
-  uint32_t *rec_of_sample;     // BinPlan::direct == 0
   float *grad_loc, *grad_attn, *grad_value;
   BinPlan p;                   // chunk_q = the forward block's units
   int slots;                   // tap slots per block: 4 wavefronts x steps x taps per step
@@ -101,10 +103,7 @@ struct TileBinner {
     stage_tiles<T>(lv, s.levels, ntc, base);
     nt = base[s.levels];
     for (int i = threadIdx.x; i < nt; i += kBlock) loff[i] = 0;
-    for (int i = threadIdx.x; i < a.slots; i += kBlock) {
-      keys[i] = kNoRecord;
-      if (!a.p.direct) stage[i].x = kNoRecord;  // slots without a record
-    }
+    for (int i = threadIdx.x; i < a.slots; i += kBlock) keys[i] = kNoRecord;
     lds_barrier();
   }
 
@@ -114,12 +113,8 @@ struct TileBinner {
     if (!ok) return;
     if (!t.in) {  // no corner inside the level: zero gradients, no record
       const size_t o = (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp;
-      if (a.p.direct) {
-        a.grad_attn[o] = 0.0f;
-        *reinterpret_cast<float2 *>(a.grad_loc + 2 * o) = make_float2(0.0f, 0.0f);
-      } else {
-        a.rec_of_sample[o] = kNoRecord;
-      }
+      a.grad_attn[o] = 0.0f;
+      *reinterpret_cast<float2 *>(a.grad_loc + 2 * o) = make_float2(0.0f, 0.0f);
       return;
     }
     const int tile = primary_tile<T>(t, ntc[l], base[l]);
@@ -165,8 +160,6 @@ struct TileBinner {
     constexpr int U = kFwdBinSlots / kBlock;
     const uint32_t *cur_row = a.cursors + static_cast<size_t>(lb_row()) * a.p.tile_bound;
     uint4 *rec = a.records + static_cast<size_t>(bm) * a.p.rec_cap;
-    const uint32_t lp_mask = (1u << a.p.lp_log2) - 1u;
-    const size_t sb = (static_cast<size_t>(b) * s.queries * s.heads + m) * s.lp;
     uint32_t slot[U], at[U], cur[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -186,20 +179,6 @@ struct TileBinner {
       // so the L2 cannot merge the partial lines; plain stores measured
       // slower (c2 forward + binning 525 -> 577 us, c4 bf16 1510 -> 1590 us)
       store_nt(rec + r, stage[slot[u]]);  // read once, by the tile kernel
-      if (!a.p.direct) keys[slot[u]] = r;  // this slot's key is not read again
-    }
-    if (!a.p.direct) {
-      // the sample -> record index in tap order: a unit's samples are
-      // consecutive slots, so a wavefront's stores cover whole lines
-      lds_barrier();
-      for (int j = threadIdx.x; j < a.slots; j += kBlock) {
-        const uint4 v = stage[j];
-        if (v.x == kNoRecord) continue;
-        const uint32_t id = v.x & kSampleMask;
-        const size_t o = sb + static_cast<size_t>(id >> a.p.lp_log2) * s.heads * s.lp +
-                         (id & lp_mask);
-        a.rec_of_sample[o] = keys[j];
-      }
     }
     // non-boundary cells of the slab's empty and split tiles listed by
     // bin_scan: tiles ch, ch + chunks, ... of the list
