@@ -587,7 +587,43 @@ def probe_library():
                                          ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.muspace_probe_atomic.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_void_p]
+    lib.muspace_probe_lds_atomic.restype = ctypes.c_int
+    lib.muspace_probe_lds_atomic.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_int, ctypes.c_void_p]
     return lib
+
+
+def run_lds_atomic_probe() -> dict:
+    """fp32 against u32 LDS atomic adds (ds_add_f32 / ds_add_u32), conflict-
+    free and scattered addresses: clocks per wavefront instruction per CU,
+    at the device's reported clock."""
+    lib = probe_library()
+    props = torch.cuda.get_device_properties(0)
+    cus = props.multi_processor_count
+    clock_hz = getattr(props, "clock_rate", 0) * 1e3 or 2.4e9
+    blocks, iters = 2 * cus, 2048
+    stream = torch.cuda.current_stream().cuda_stream
+    out = torch.empty(blocks * 1024, dtype=torch.int32, device="cuda")
+    rows = {}
+    for kind, name in ((0, "f32_conflict_free"), (1, "u32_conflict_free"),
+                       (2, "f32_scattered"), (3, "u32_scattered")):
+        def launch():
+            rc = lib.muspace_probe_lds_atomic(out.data_ptr(), blocks, iters, kind, stream)
+            assert rc == 0, rc
+        launch()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        launch()
+        end.record()
+        end.synchronize()
+        ms = start.elapsed_time(end)
+        wave_instr_per_cu = blocks * 16 * iters / cus
+        row = {"ms": round(ms, 3),
+               "clk_per_wave_instr_per_cu": round(ms * 1e-3 * clock_hz / wave_instr_per_cu, 2)}
+        rows[name] = row
+        print(f"[probe] lds atomic {name}: {row}", file=sys.stderr, flush=True)
+    return {"lds_atomic_probe": rows}
 
 
 PROBE_MIB = (1, 2, 4, 8, 16)  # footprint per XCD
@@ -667,6 +703,8 @@ def main() -> int:
     parser.add_argument("--gather-probe", action="store_true",
                         help="only the random 128-byte line gather probe (the forward's "
                              "corner-gather ceiling), then exit")
+    parser.add_argument("--lds-atomic-probe", action="store_true",
+                        help="time fp32 against u32 LDS atomic adds and exit")
     parser.add_argument("--atomic-probe", action="store_true",
                         help="only the line-wide fp32 atomic-add probe, then exit")
     parser.add_argument("--sca-only", action="store_true",
@@ -703,11 +741,13 @@ def main() -> int:
         print(json.dumps({"copy_probe_bytes": n * 4, "launches": 5}))
         return 0
 
-    if args.gather_probe or args.atomic_probe:
+    if args.gather_probe or args.atomic_probe or args.lds_atomic_probe:
         out = {}
         for kind, wanted in (("gather", args.gather_probe), ("atomic", args.atomic_probe)):
             if wanted:
                 out.update(run_probe(kind))
+        if args.lds_atomic_probe:
+            out.update(run_lds_atomic_probe())
         print(json.dumps(out))
         return 0
 

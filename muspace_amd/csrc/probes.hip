@@ -1,11 +1,14 @@
 // Memory-system probes of libmuspace_probes.so (bench.py --gather-probe,
-// --atomic-probe). They measure the two ceilings the MSDA kernels are priced
-// against on MI355X and are not part of the MSDA library:
+// --atomic-probe, --lds-atomic-probe). They measure the ceilings the MSDA
+// kernels are priced against on MI355X and are not part of the MSDA library:
 //
-//   gather  random 128-byte line reads, 16 bytes per lane (8 lanes per line),
-//           the rate of the forward's corner-row gathers;
-//   atomic  line-wide fp32 atomic adds (32 lanes on one 128-byte line), the
-//           rate of a reference-style atomic grad_value scatter.
+//   gather      random 128-byte line reads, 16 bytes per lane (8 lanes per
+//               line), the rate of the forward's corner-row gathers;
+//   atomic      line-wide fp32 atomic adds (32 lanes on one 128-byte line),
+//               the rate of a reference-style atomic grad_value scatter;
+//   lds atomic  fp32 (ds_add_f32) and u32 (ds_add_u32) atomic adds to LDS,
+//               bank-conflict-free or scattered addresses, the rate an
+//               LDS-accumulated grad_value would run at.
 //
 // Each workgroup works in the region of the XCD it runs on (hardware
 // register XCC_ID), so `lines` per XCD sets the footprint one L2 sees.
@@ -66,6 +69,32 @@ __global__ void __launch_bounds__(kProbeBlock)
   }
 }
 
+// kind bit 0: u32 (else fp32) adds; bit 1: scattered (else consecutive,
+// bank-conflict-free) addresses. Every index is masked into the 8192-word
+// array; out[] gets one word per thread.
+template <typename T>
+__device__ __forceinline__ void lds_atomic_body(T *out, int iters, bool scattered) {
+  __shared__ T s[8192];
+  for (int i = threadIdx.x; i < 8192; i += blockDim.x) s[i] = T(0);
+  __syncthreads();
+  const uint32_t t = threadIdx.x;
+  for (int it = 0; it < iters; ++it) {
+    const uint32_t a = scattered ? mix(t * 8191u + static_cast<uint32_t>(it)) & 8191u
+                                 : (t + 97u * static_cast<uint32_t>(it)) & 8191u;
+    atomicAdd(&s[a], T(1));
+  }
+  __syncthreads();
+  out[blockIdx.x * blockDim.x + threadIdx.x] = s[t];
+}
+
+__global__ void __launch_bounds__(1024) probe_lds_atomic(uint32_t *out, int iters, int kind) {
+  if (kind & 1) {
+    lds_atomic_body<uint32_t>(out, iters, (kind & 2) != 0);
+  } else {
+    lds_atomic_body<float>(reinterpret_cast<float *>(out), iters, (kind & 2) != 0);
+  }
+}
+
 bool bad_args(const void *buf, uint64_t lines, int blocks, int iters) {
   return buf == nullptr || lines == 0 || lines > (uint64_t{1} << 26) || blocks <= 0 ||
          iters <= 0;
@@ -96,6 +125,18 @@ __attribute__((visibility("default"))) int muspace_probe_atomic(float *buf, uint
   if (bad_args(buf, lines, blocks, iters)) return hipErrorInvalidValue;
   probe_atomic<<<blocks, kProbeBlock, 0, static_cast<hipStream_t>(stream)>>>(
       buf, static_cast<uint32_t>(lines), iters);
+  return hipGetLastError();
+}
+
+// blocks workgroups of 1024 threads, each thread `iters` LDS atomic adds
+// (kind as probe_lds_atomic); out: blocks * 1024 words. Returns a hipError_t.
+__attribute__((visibility("default"))) int muspace_probe_lds_atomic(uint32_t *out, int blocks,
+                                                                    int iters, int kind,
+                                                                    void *stream) {
+  if (out == nullptr || blocks <= 0 || iters <= 0 || kind < 0 || kind > 3) {
+    return hipErrorInvalidValue;
+  }
+  probe_lds_atomic<<<blocks, 1024, 0, static_cast<hipStream_t>(stream)>>>(out, iters, kind);
   return hipGetLastError();
 }
 
