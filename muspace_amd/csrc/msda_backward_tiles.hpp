@@ -117,8 +117,7 @@ __host__ __device__ constexpr size_t tile_lds_bytes() {
          static_cast<size_t>(K) * 16 +                     // sorted records
          static_cast<size_t>(4 * NPOS) * 4 +               // position count, offset, rank table
          2 * 64 * 4 +                                      // count buckets, bucket starts
-         16 * 4 +                                          // per-wavefront count totals
-         static_cast<size_t>(C) * 4;                       // zero slot
+         16 * 4;                                           // per-wavefront count totals
 }
 
 // Per-level tile table in LDS: level l owns tiles [base[l], base[l+1]).
@@ -721,8 +720,7 @@ __global__ void __launch_bounds__(kTileBlock)
   VT *vt = reinterpret_cast<VT *>(lds);  // NPOS cells + one zero row
   float *planes = reinterpret_cast<float *>(lds + static_cast<size_t>(NPOS + 1) * C * VB);
   uint4 *stash = reinterpret_cast<uint4 *>(planes + 4 * NPOS * C);
-  float *dummy = reinterpret_cast<float *>(stash + K);  // [C], always zero (16-byte aligned)
-  uint32_t *pcount = reinterpret_cast<uint32_t *>(dummy + C);
+  uint32_t *pcount = reinterpret_cast<uint32_t *>(stash + K);
   uint32_t *poff = pcount + NPOS;
   // rank table: rank r -> {count << 16 | position, first slot}
   uint2 *rtab = reinterpret_cast<uint2 *>(poff + NPOS);
@@ -859,42 +857,77 @@ __global__ void __launch_bounds__(kTileBlock)
       if (unit < NPOS * UPV) reinterpret_cast<uint4 *>(vt)[unit] = vt_next[v];
     }
   };
-  // cell sums of a finished item's corner planes to grad_value (slots that
-  // map to row or column -1 only ever hold contributions of invalid corners
-  // and are not read); four channels per thread and step
+  // cell sums of a finished item's corner planes to grad_value: cell (r, c)
+  // of [0, T]^2 sums slot (r - dy, c - dx) of plane (dy, dx) (slots that map
+  // to row or column -1 only ever hold contributions of invalid corners and
+  // are not read). Cells the item owns alone get one 16-byte store per four
+  // channels; cells it shares with a neighbouring tile's items (the halo row
+  // and column, the first row and column away from the level's edge, every
+  // cell of a split tile) are added with fp32 atomics, one channel per lane,
+  // so that one atomic instruction covers whole 128-byte lines (four channels
+  // per lane put a lane every 16 bytes and took four instructions per line).
   auto write_back = [&](const Item &d) {
     constexpr int C4 = C / 4;
     const TileGeom g = item_geom(d);
     const Level Lw = lv[g.l];
     const bool split = (d.tile & kSplitBit) != 0;
     const size_t slab = slab_offset(d);
-    for (int i = tid; i < NPOS * C4; i += kTileBlock) {
-      const int cell = i / C4, ch = (i % C4) * 4;
-      const int r = cell / TV, c = cell % TV;  // cell (r, c) of [0, T]^2
-      const int y = g.y_lo + r, x = g.x_lo + c;
-      if (y >= Lw.h || x >= Lw.w) continue;
-      float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto cell_ptr = [&](int r, int c) {
+      return grad_value + slab +
+             static_cast<size_t>(Lw.start + (g.y_lo + r) * Lw.w + g.x_lo + c) * MC;
+    };
+    if (!split) {
+      for (int i = tid; i < T * T * C4; i += kTileBlock) {
+        const int cell = i / C4, ch = (i % C4) * 4;
+        const int r = cell / T, c = cell % T;
+        if (g.y_lo + r >= Lw.h || g.x_lo + c >= Lw.w || boundary_cell(r, c, g)) continue;
+        float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int pr = r - (q >> 1), pc = c - (q & 1);  // position, >= -1
+          const float4 v = *reinterpret_cast<const float4 *>(
+              planes + (q * NPOS + (pr + 1) * TV + pc + 1) * C + ch);
+          sum.x += v.x;
+          sum.y += v.y;
+          sum.z += v.z;
+          sum.w += v.w;
+        }
+        const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
+        store16_nt(cell_ptr(r, c) + ch, sv);
+      }
+    }
+    // shared cells, enumerated: split tiles all of [0, T]^2; otherwise row T
+    // (T + 1 cells), column T above it (T), then row 0 if the tile is not at
+    // the level's top (T) and column 0 below that row if not at its left
+    const int top = g.y_lo > 0 ? 1 : 0, left = g.x_lo > 0 ? 1 : 0;
+    const int n_shared = split ? NPOS : TV + T + top * T + left * (T - top);
+    for (int i = tid; i < n_shared * C; i += kTileBlock) {
+      const int k = i / C, ch = i % C;
+      int r, c;
+      if (split) {
+        r = k / TV;
+        c = k % TV;
+      } else if (k < TV) {
+        r = T;
+        c = k;
+      } else if (k < TV + T) {
+        r = k - TV;
+        c = T;
+      } else if (top && k < TV + 2 * T) {
+        r = 0;
+        c = k - TV - T;
+      } else {
+        r = top + (k - TV - T - top * T);
+        c = 0;
+      }
+      if (g.y_lo + r >= Lw.h || g.x_lo + c >= Lw.w) continue;
+      float sum = 0.0f;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int pr = r - (q >> 1), pc = c - (q & 1);  // position, >= -1
-        const float4 v = *reinterpret_cast<const float4 *>(
-            pr < T && pc < T ? planes + (q * NPOS + (pr + 1) * TV + pc + 1) * C + ch
-                             : dummy + ch);  // always zero
-        sum.x += v.x;
-        sum.y += v.y;
-        sum.z += v.z;
-        sum.w += v.w;
+        if (pr < T && pc < T) sum += planes[(q * NPOS + (pr + 1) * TV + pc + 1) * C + ch];
       }
-      float *dst = grad_value + slab + static_cast<size_t>(Lw.start + y * Lw.w + x) * MC + ch;
-      if (!split && r < T && c < T && !boundary_cell(r, c, g)) {
-        const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
-        store16_nt(dst, sv);
-      } else {
-        unsafeAtomicAdd(dst, sum.x);
-        unsafeAtomicAdd(dst + 1, sum.y);
-        unsafeAtomicAdd(dst + 2, sum.z);
-        unsafeAtomicAdd(dst + 3, sum.w);
-      }
+      unsafeAtomicAdd(cell_ptr(r, c) + ch, sum);
     }
   };
 
@@ -905,7 +938,6 @@ __global__ void __launch_bounds__(kTileBlock)
   load_value_tile(c0.d, true);
   store_value_tile();
   if (tid < UPV) reinterpret_cast<uint4 *>(vt + NPOS * C)[tid] = make_uint4(0u, 0u, 0u, 0u);
-  if (tid < C) dummy[tid] = 0.0f;
   if (tid < NPOS) pcount[tid] = 0;
   if (tid < kWave) bucket[tid] = 0;
   __syncthreads();
