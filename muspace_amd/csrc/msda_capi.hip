@@ -680,10 +680,13 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   if (static_cast<int64_t>(s.queries) * s.heads * s.channels >= (int64_t{1} << 32)) return false;
   p.rec_cap = static_cast<int64_t>(s.queries) * s.lp;
   // Direct gradient writes scatter 12 bytes per sample over the slab's span of
-  // queries * lp samples; they pay when that span fits one XCD's 4 MB L2,
-  // where partial lines merge before they reach HBM (measured: c2 3.8 MB and
-  // c3 1.9 MB 5% and 11% faster; c1 4.3 MB and c4 5.8 MB 2% slower).
-  p.direct = p.rec_cap * 12 <= (4 << 20) ? 1 : 0;
+  // queries * lp samples; the records path instead stores them over the
+  // records and msda_grad_gather un-sorts them, one random 16-byte read per
+  // sample. Measured with the current kernels (full steps, direct writes also
+  // taking the fused forward): c2 (3.8 MB) and c3 (1.9 MB) 5% and 11% faster
+  // direct, c1 (4.3 MB) 1.4% and c4 (5.8 MB) 1.2% faster direct. Spans past
+  // 8 MB keep the records path (not measured there).
+  p.direct = p.rec_cap * 12 <= (8 << 20) ? 1 : 0;
   if (p.rec_cap >= (int64_t{1} << 31)) return false;
   const int64_t bm = static_cast<int64_t>(s.batch) * s.heads;
   // records per work item (a tile with more is split into items whose cells
@@ -798,10 +801,9 @@ bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const in
   constexpr int value_dtype = std::is_same<VT, float>::value ? MUSPACE_DTYPE_F32
                                                              : MUSPACE_DTYPE_F16;
   // Only where the tile kernel writes the location and weight gradients
-  // straight to sample order: with the records-plus-gather path (c1, c4)
-  // the fused forward also stores the sample -> record index, and at c4
-  // its LDS leaves two blocks per CU where the 16-bit forward keeps three
-  // (fused c4 bf16 step 2969 against 2953 us with the binning kernels).
+  // straight to sample order: the records-plus-gather path would also need
+  // the sample -> record index, which the fused forward measured slower to
+  // store than bin_scatter does.
   if (!w.plan.direct) return false;
   int units = 0, slots = 0;
   if (!fwd_bin_chunk(s, value_dtype, units, slots)) return false;

@@ -247,12 +247,12 @@ def test_fused_forward_binning_matches_oracle(native_lib, case, dtypes):
 
 
 def test_fused_forward_binning_records_path_matches_oracle(native_lib):
-    """A slab span of queries x L*P x 12 bytes above 4 MB: the tile kernel
+    """A slab span of queries x L*P x 12 bytes above 8 MB: the tile kernel
     stores the location and weight gradients over the records and
     msda_grad_gather copies them into sample order through the sample ->
     record index, so ms_deform_attn_forward_bin runs the plain forward and
     the binning kernels instead of the fused forward."""
-    case = (1, 11000, 2, 32, ((20, 30),), 32)
+    case = (1, 22000, 2, 32, ((20, 30),), 32)
     print(f"[parity] fused records path {_id(case)}", flush=True)
     t, grad = small_case(91, *case)
     out, gv, gl, ga = run_fused(native_lib, t, grad, torch.float32, torch.float32)
