@@ -153,6 +153,17 @@ class Step:
         mark("rest1", main)
 
 
+def fused_binning(lib, cfg, value_dtype) -> bool:
+    """Whether ms_deform_attn_forward_bin stores the backward's records from
+    the forward kernel at this config (else the plain forward and the
+    binning kernels run in that call)."""
+    value = torch.empty((cfg.batch, cfg.spatial_size, cfg.heads, cfg.channels),
+                        dtype=value_dtype, device="meta")
+    loc = torch.empty((cfg.batch, cfg.queries, cfg.heads, cfg.num_levels, cfg.points, 2),
+                      device="meta")
+    return lib.forward_bin_fuses(value, loc)
+
+
 def time_steps(step: Step, steps: int, warmup: int, per_kernel: bool = True,
                repeats: int = 5) -> dict:
     """Time exactly `steps` steps after `warmup`, as `repeats` back-to-back
@@ -798,6 +809,7 @@ def main() -> int:
                 "alloc_us": round(r["zero_ms"] * 1e3, 1),
                 "effective_GBps": round((f + b) / (r["ms_per_step"] * 1e-3) / 1e9, 1),
                 "side_stream_binning_fwd_bwd_us": round(r_side["ms_per_step"] * 1e3, 1),
+                "forward_kernel_stores_records": fused_binning(lib, c, vdt),
             }
             torch.cuda.empty_cache()
         # the earlier schedule at the headline config: binning kernels on a
@@ -867,6 +879,7 @@ def main() -> int:
             "bin_us": round(res["bin_ms"] * 1e3, 1),
             "rest_us": round(res["rest_ms"] * 1e3, 1),
             "alloc_us": round(res["zero_ms"] * 1e3, 1),
+            "forward_kernel_stores_records": fused_binning(lib, cfg, torch.float32),
             "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
             "algorithmic_bytes": {"fwd": fwd_b, "bwd": bwd_b},
         },

@@ -190,6 +190,17 @@ MUSPACE_API int ms_deform_attn_forward_bin(
     int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
     size_t workspace_bytes, void *stream);
 
+/* 1 if ms_deform_attn_forward_bin, given 16-byte-aligned tensors and a
+ * 256-byte-aligned workspace of ms_deform_attn_backward_workspace_size bytes,
+ * stores the backward's records from the forward kernel for these dims; 0 if
+ * it runs ms_deform_attn_forward and the binning kernels instead (or the
+ * shape takes the atomic backward). Results are the same either way. No
+ * reference counterpart. */
+MUSPACE_API int ms_deform_attn_forward_bin_fused(int value_dtype, int64_t batch,
+                                                 int64_t spatial_size, int64_t num_heads,
+                                                 int64_t channels, int64_t num_levels,
+                                                 int64_t num_query, int64_t num_point);
+
 /* BEVFormer spatial cross-attention, one camera, with the scatter-average
  * fused into the forward: for the camera-rebatched
  *   value               [batch*num_cams, spatial_size, num_heads, channels]  value_dtype

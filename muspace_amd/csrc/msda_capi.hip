@@ -788,6 +788,21 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   }
 }
 
+// Whether ms_deform_attn_forward_bin stores the records from the forward
+// kernel for shape s (given a planned tile workspace w): only where the tile
+// kernel writes the location and weight gradients straight to sample order
+// (the records-plus-gather path would also need the sample -> record index,
+// which the fused forward measured slower to store than bin_scatter does),
+// within the block's tap slots and its LDS budget. units, slots: the
+// forward block's queries and tap slots.
+bool fwd_bin_fuses(const msda::Shape &s, int value_dtype, const TileWorkspace &w, int &units,
+                   int &slots) {
+  if (!w.plan.direct) return false;
+  if (!fwd_bin_chunk(s, value_dtype, units, slots)) return false;
+  return slots <= msda::kFwdBinSlots &&
+         msda::fwd_bin_lds_bytes(slots, w.plan.tile_bound) <= msda::kFwdBinDynLds;
+}
+
 // The forward with the backward's binning fused in (msda_forward_bin.hpp):
 // bin_count and bin_scan over the forward blocks' query chunks, then the
 // forward row kernel, which also stores every chunk's records. Launches
@@ -800,17 +815,8 @@ bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const in
   constexpr int T = msda::TileCfg<VT, C>::T;
   constexpr int value_dtype = std::is_same<VT, float>::value ? MUSPACE_DTYPE_F32
                                                              : MUSPACE_DTYPE_F16;
-  // Only where the tile kernel writes the location and weight gradients
-  // straight to sample order: the records-plus-gather path would also need
-  // the sample -> record index, which the fused forward measured slower to
-  // store than bin_scatter does.
-  if (!w.plan.direct) return false;
   int units = 0, slots = 0;
-  if (!fwd_bin_chunk(s, value_dtype, units, slots)) return false;
-  if (slots > msda::kFwdBinSlots ||
-      msda::fwd_bin_lds_bytes(slots, w.plan.tile_bound) > msda::kFwdBinDynLds) {
-    return false;
-  }
+  if (!fwd_bin_fuses(s, value_dtype, w, units, slots)) return false;
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + w.counts);
   uint32_t *tile_start = reinterpret_cast<uint32_t *>(ws + w.tile_start);
@@ -1256,6 +1262,22 @@ size_t ms_deform_attn_backward_workspace_size(int value_dtype, int64_t batch,
   TileWorkspace w;
   if (!needs_data(s) || s.lp == 0 || !plan_tile_workspace(s, value_dtype, w)) return 0;
   return w.bytes;
+}
+
+int ms_deform_attn_forward_bin_fused(int value_dtype, int64_t batch, int64_t spatial_size,
+                                     int64_t num_heads, int64_t channels, int64_t num_levels,
+                                     int64_t num_query, int64_t num_point) {
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               batch > 0 ? batch : 1};
+  msda::Shape s;
+  if (validate("ms_deform_attn_forward_bin_fused", a, value_dtype, value_dtype, s)) return 0;
+  ok();
+  TileWorkspace w;
+  int units = 0, slots = 0;
+  return needs_data(s) && s.lp > 0 && plan_tile_workspace(s, value_dtype, w) &&
+                 fwd_bin_fuses(s, value_dtype, w, units, slots)
+             ? 1
+             : 0;
 }
 
 int ms_deform_attn_backward_ws(const void *value, int value_dtype, const int64_t *spatial_shapes,

@@ -63,6 +63,7 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         + [_c_ptr],
     ),
     "ms_deform_attn_backward_workspace_size": (ctypes.c_size_t, [_c_int] + [_c_int64] * 7),
+    "ms_deform_attn_forward_bin_fused": (_c_int, [_c_int] + [_c_int64] * 7),
     "ms_deform_attn_backward_bin": (
         _c_int,
         [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
@@ -211,6 +212,7 @@ class NativeLibrary:
             "ms_deform_attn_backward_bin": self.ms_deform_attn_backward_bin,
             "ms_deform_attn_backward_rest": self.ms_deform_attn_backward_rest,
             "ms_deform_attn_forward_bin": self.ms_deform_attn_forward_bin,
+            "forward_bin_fuses": self.forward_bin_fuses,
             "ms_deform_attn_forward_softmax": self.ms_deform_attn_forward_softmax,
             "ms_deform_attn_backward_softmax": self.ms_deform_attn_backward_softmax,
             "backward_softmax_workspace": self.backward_softmax_workspace,
@@ -447,6 +449,15 @@ class NativeLibrary:
     def backward_softmax_workspace_bytes(self, value, sampling_locations) -> int:
         """Scratch bytes of the softmax backward for these shapes."""
         return self._workspace_bytes(value, sampling_locations, softmax=True)
+
+    def forward_bin_fuses(self, value, sampling_locations) -> bool:
+        """Whether :meth:`ms_deform_attn_forward_bin` stores the backward's
+        records from the forward kernel for these shapes (else it runs the
+        plain forward and the binning kernels; same results)."""
+        batch, spatial, heads, channels = value.shape
+        _, queries, _, levels, points, _ = sampling_locations.shape
+        return bool(self._raw["ms_deform_attn_forward_bin_fused"](
+            _dtype_code(value.dtype), batch, spatial, heads, channels, levels, queries, points))
 
     def backward_workspace(self, value, sampling_locations):
         """Scratch of the tile-owned backward for these shapes (1 byte when the

@@ -255,6 +255,7 @@ def test_fused_forward_binning_records_path_matches_oracle(native_lib):
     case = (1, 22000, 2, 32, ((20, 30),), 32)
     print(f"[parity] fused records path {_id(case)}", flush=True)
     t, grad = small_case(91, *case)
+    assert not native_lib.forward_bin_fuses(t["value"], t["sampling_locations"])
     out, gv, gl, ga = run_fused(native_lib, t, grad, torch.float32, torch.float32)
     torch.cuda.synchronize()
     o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
@@ -407,6 +408,9 @@ def _check_full_config(native_lib, name, value_dtype, geometry_dtype, fused):
     t = make_inputs(cfg, value_dtype=torch.float32)
     grad = t.pop("grad_output")
     if fused:
+        # the forward kernel itself stores the records here (no fallback to
+        # the binning kernels)
+        assert native_lib.forward_bin_fuses(t["value"].to(value_dtype), t["sampling_locations"])
         out, gv, gl, ga = run_fused(native_lib, t, grad, value_dtype, geometry_dtype)
         plain = run_forward(native_lib, t, value_dtype, geometry_dtype)
         torch.cuda.synchronize()
