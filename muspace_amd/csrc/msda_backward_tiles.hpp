@@ -600,34 +600,89 @@ __device__ __forceinline__ uint32_t item_batches(const Item &d) {
   return (d.r1 - d.r0 + K - 1) / K;
 }
 
-// Eight channels per lane: 32 bytes of fp32 (two 16-byte accesses) or 16
-// bytes of fp16/bf16 (works on LDS and global pointers).
-__device__ __forceinline__ void load8ch(const float *p, float (&o)[8]) {
+// One lane's eight channels of a value or grad_out row in the owner loop:
+// fp32 as floats; fp16/bf16 kept packed (16 bytes), so that the corner dot
+// products take one v_dot2 (two products, fp32 sum) per channel pair and
+// only the corner sums need the channels as floats (c4 tile kernel: bf16
+// 1468 -> 1445 us, fp16 1512 -> 1451 us against decoded rows and FMAs).
+template <typename VT>
+struct Row8 {
+  float f[8];
+};
+template <>
+struct Row8<bf16_t> {
+  u32x4 w;
+};
+template <>
+struct Row8<__half> {
+  u32x4 w;
+};
+
+// row from LDS (16-byte aligned)
+__device__ __forceinline__ void lds_row8(const float *p, Row8<float> &o) {
   const float4 a = reinterpret_cast<const float4 *>(p)[0];
   const float4 b = reinterpret_cast<const float4 *>(p)[1];
-  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
-  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  o.f[0] = a.x; o.f[1] = a.y; o.f[2] = a.z; o.f[3] = a.w;
+  o.f[4] = b.x; o.f[5] = b.y; o.f[6] = b.z; o.f[7] = b.w;
 }
-__device__ __forceinline__ void load8ch(const bf16_t *p, float (&o)[8]) { load16(p, o); }
-__device__ __forceinline__ void load8ch(const __half *p, float (&o)[8]) { load16(p, o); }
-
-// Eight channels at byte offset `off` of a buffer (32-bit offsets: fewer
-// address instructions than 64-bit pointers).
 template <typename VT>
-__device__ __forceinline__ void buffer_load8ch(__amdgpu_buffer_rsrc_t r, uint32_t off,
-                                               float (&o)[8]) {
-  if constexpr (sizeof(VT) == 4) {
-    float a[4], b[4];
-    decode16(VT(), buffer_load16(r, off), a);
-    decode16(VT(), buffer_load16(r, off + 16), b);
+__device__ __forceinline__ void lds_row8(const VT *p, Row8<VT> &o) {
+  o.w = *reinterpret_cast<const u32x4 *>(p);
+}
+
+// row at byte offset `off` of a buffer (32-bit offsets: fewer address
+// instructions than 64-bit pointers)
+__device__ __forceinline__ void buf_row8(__amdgpu_buffer_rsrc_t r, uint32_t off, Row8<float> &o) {
+  float a[4], b[4];
+  decode16(float(), buffer_load16(r, off), a);
+  decode16(float(), buffer_load16(r, off + 16), b);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o[j] = a[j];
-      o[4 + j] = b[j];
-    }
-  } else {
-    decode16(VT(), buffer_load16(r, off), o);
+  for (int j = 0; j < 4; ++j) {
+    o.f[j] = a[j];
+    o.f[4 + j] = b[j];
   }
+}
+template <typename VT>
+__device__ __forceinline__ void buf_row8(__amdgpu_buffer_rsrc_t r, uint32_t off, Row8<VT> &o) {
+  o.w = buffer_load16(r, off);
+}
+
+// sum over the eight channels of a[j] * b[j]
+__device__ __forceinline__ float dot8(const Row8<float> &a, const Row8<float> &b) {
+  float d = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) d += a.f[j] * b.f[j];
+  return d;
+}
+__device__ __forceinline__ float dot8(const Row8<bf16_t> &a, const Row8<bf16_t> &b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const uint32_t x[4] = {a.w.x, a.w.y, a.w.z, a.w.w}, y[4] = {b.w.x, b.w.y, b.w.z, b.w.w};
+  float d = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x[i]),
+                                        __builtin_bit_cast(bf16x2, y[i]), d, false);
+  return d;
+}
+__device__ __forceinline__ float dot8(const Row8<__half> &a, const Row8<__half> &b) {
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  const uint32_t x[4] = {a.w.x, a.w.y, a.w.z, a.w.w}, y[4] = {b.w.x, b.w.y, b.w.z, b.w.w};
+  float d = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x[i]), __builtin_bit_cast(f16x2, y[i]),
+                               d, false);
+  return d;
+}
+
+// the eight channels as floats (channel j of the lane -> o[j])
+__device__ __forceinline__ void floats8(const Row8<float> &a, float (&o)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = a.f[j];
+}
+template <typename VT>
+__device__ __forceinline__ void floats8(const Row8<VT> &a, float (&o)[8]) {
+  decode16(VT(), a.w, o);
 }
 
 // The four corner dot products of one record, D_d = sum over the group's KQ
@@ -706,6 +761,13 @@ __global__ void __launch_bounds__(kTileBlock)
   constexpr int VPT = (NPOS * UPV + kTileBlock - 1) / kTileBlock;  // value units per thread
   constexpr int RPT = K / kTileBlock;  // records per thread
   constexpr int NR = 2;                // grad_out rows in flight per group
+  // owners' corner sums as MFMA outer products (needs whole 4-lane groups):
+  // for 16-bit values, whose owner loop also decodes each grad_out row
+  // (c4 tile kernel: bf16 1515 -> 1469 us, fp16 1650 -> 1511 us, before the
+  // packed dots and the request order below); fp32 values keep the vector
+  // FMAs, which measured faster there (c2 536 against 547 us, c1 191
+  // against 196 us)
+  constexpr bool kMfmaSums = KQ >= 4 && sizeof(VT) == 2;
   // teams of up to 4 groups inside one 16-lane DPP row
   constexpr int kMaxTeamShift = KQ <= 4 ? 2 : 1;
   static_assert(CPL == 8 && (KQ == 2 || KQ == 4 || KQ == 8), "bad lane layout");
@@ -1108,11 +1170,12 @@ __global__ void __launch_bounds__(kTileBlock)
       const int p_id = static_cast<int>(rt.x & 0xffffu);
       const uint32_t n = rt.x >> 16;
       if (n == 0 && !first_of_item) break;  // positions are in order of decreasing count
-      float acc[4][CPL];
+      // acc[j][d]: corner d's sum of this lane's channel k * CPL + j (an
+      // MFMA accumulator per j; packing separate floats into one per MFMA
+      // measured 10% slower for 16-bit values)
+      f32x4 acc[CPL];
 #pragma unroll
-      for (int d = 0; d < 4; ++d)
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) acc[d][j] = 0.0f;
+      for (int j = 0; j < CPL; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       // this group's records of the position: sub, sub + S, ...
       const uint32_t cnt = n > static_cast<uint32_t>(sub)
                                ? (n - static_cast<uint32_t>(sub) + S - 1) >> tshift
@@ -1122,49 +1185,105 @@ __global__ void __launch_bounds__(kTileBlock)
         const uint32_t stride = static_cast<uint32_t>(S);
         const int py = p_id / TV - 1, px = p_id % TV - 1;  // tile frame, >= -1
         // corner value rows (row -1 or column -1: the zero row after the tile)
-        float v[4][CPL];
+        Row8<VT> v[4];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
           const int cy = py + (d >> 1), cx = px + (d & 1);
-          load8ch(vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * C : NPOS * C) + k * CPL, v[d]);
+          lds_row8(vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * C : NPOS * C) + k * CPL, v[d]);
         }
-        auto one_record = [&](const u32x4 &e, const float (&gv)[CPL], uint32_t slot) {
+        // One record: its four corner dot products (stored over its stash
+        // slot) and, except where the MFMA sums run, its corner sums. With
+        // MFMA sums the record's decoded row and its corner weight for this
+        // lane are returned in gv, wk for the caller's sums, which come
+        // after the group's next row is requested.
+        auto one_record = [&](const u32x4 &e, const Row8<VT> &gr, uint32_t slot,
+                              float (&gv)[CPL], float &wk) {
           const float wx1 = __uint_as_float(e.y);
           const float ay0 = __uint_as_float(e.z), ay1 = __uint_as_float(e.w);
           const float wx0 = 1.0f - wx1;
-          const float wa[4] = {ay0 * wx0, ay0 * wx1, ay1 * wx0, ay1 * wx1};
           float dd[4];
+          if constexpr (sizeof(VT) == 4) {
+            // fp32 rows: corner sums and dots in one pass over the row (at
+            // the kernel's register limit: a copy of the row, to request the
+            // next one before the sums, spills)
+            const float wa[4] = {ay0 * wx0, ay0 * wx1, ay1 * wx0, ay1 * wx1};
 #pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            dd[d] = 0.0f;
+            for (int d = 0; d < 4; ++d) {
+              dd[d] = 0.0f;
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-              acc[d][j] += wa[d] * gv[j];
-              dd[d] += gv[j] * v[d][j];
+              for (int j = 0; j < CPL; ++j) {
+                acc[j][d] += wa[d] * gr.f[j];
+                dd[d] += gr.f[j] * v[d].f[j];
+              }
+            }
+          } else {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) dd[d] = dot8(gr, v[d]);
+            floats8(gr, gv);
+            if constexpr (kMfmaSums) {
+              wk = ((k & 2) ? ay1 : ay0) * ((k & 1) ? wx1 : wx0);
+            } else {
+              const float wa[4] = {ay0 * wx0, ay0 * wx1, ay1 * wx0, ay1 * wx1};
+#pragma unroll
+              for (int j = 0; j < CPL; ++j)
+#pragma unroll
+                for (int d = 0; d < 4; ++d) acc[j][d] += wa[d] * gv[j];
             }
           }
           // D_0..D_3 replace the consumed record (read by this group alone)
           store_corner_dots<KQ>(dd, k, stash_f + slot * 4);
         };
         // NR records in flight: register set j holds this group's record
-        // r + j and is refilled with record r + j + NR as soon as it is
-        // consumed. Past the end of the list a set keeps its (consumed)
-        // record: a processed slot holds D values, not a record id.
+        // r + j and, once the record's row has been used, is refilled with
+        // record r + j + NR (stash entry read, row requested). The MFMA sums
+        // of record r + j come after that request: the chain of a
+        // position's rows is what the phase waits on (c4 bf16 tile kernel
+        // 1446 -> 1382 us against sums before the request; requesting before
+        // the dots, from a copy of the row, measured 4% slower than after
+        // them). Past the end of the list a set keeps its record: a
+        // processed slot holds D values, not a record id.
         u32x4 e[NR];
-        float g[NR][CPL];
+        Row8<VT> g[NR];
 #pragma unroll
         for (int j = 0; j < NR; ++j) {
           e[j] = vstash[first + stride * min(static_cast<uint32_t>(j), cnt - 1)];
-          buffer_load8ch<VT>(grsrc, grow(e[j].x), g[j]);
+          buf_row8(grsrc, grow(e[j].x), g[j]);
+          // requests in set order: the loop waits for set j's row by its
+          // place in the in-order vmcnt, which holds only if set 0's row
+          // went out first (the compiler issued set 1's first, and every
+          // record then waited for both rows: c4 bf16 tile kernel 1378 ->
+          // 1330 us with the order kept, c2 fp32 556 -> 533 us)
+          __builtin_amdgcn_sched_barrier(0);
         }
         for (uint32_t r = 0; r < cnt; r += NR) {
 #pragma unroll
           for (int j = 0; j < NR; ++j) {
-            if (r + j < cnt) one_record(e[j], g[j], first + stride * (r + j));
+            const bool live = r + j < cnt;
+            float gv[CPL];
+            float wk = 0.0f;
+            if (live) one_record(e[j], g[j], first + stride * (r + j), gv, wk);
             const uint32_t nx = r + j + NR;
             const u32x4 t = vstash[first + stride * min(nx, cnt - 1)];
             e[j] = nx < cnt ? t : e[j];
-            buffer_load8ch<VT>(grsrc, grow(e[j].x), g[j]);
+            buf_row8(grsrc, grow(e[j].x), g[j]);
+            if constexpr (kMfmaSums) {
+              // corner sums on the matrix cores: v_mfma_f32_4x4x1f32 is 16
+              // independent 4 x 4 outer products, block b on lanes
+              // 4b..4b+3 (A[i] from lane 4b + i, B[j] from lane 4b + j,
+              // D[i][j] in register i of lane 4b + j). A lane group of
+              // KQ >= 4 lanes is KQ / 4 whole blocks: lane k gives corner
+              // (k & 3)'s weight as A and its channel k * CPL + j as B, so
+              // register d of lane k gets w_d * g[k * CPL + j] -- acc[j][d]
+              // -- at twice the rate of the vector FMAs and off the vector
+              // pipe. A block is one group's lanes only, and the result is
+              // written under EXEC, so a group that has run out of records
+              // keeps its sums.
+              if (live) {
+#pragma unroll
+                for (int jj = 0; jj < CPL; ++jj)
+                  acc[jj] = __builtin_amdgcn_mfma_f32_4x4x1f32(wk, gv[jj], acc[jj], 0, 0, 0);
+              }
+            }
           }
         }
       }
@@ -1174,14 +1293,14 @@ __global__ void __launch_bounds__(kTileBlock)
 #pragma unroll
         for (int d = 0; d < 4; ++d)
 #pragma unroll
-          for (int j = 0; j < CPL; ++j) acc[d][j] += MSDA_DPP(acc[d][j], 0x120 + KQ);
+          for (int j = 0; j < CPL; ++j) acc[j][d] += MSDA_DPP(acc[j][d], 0x120 + KQ);
       }
       if constexpr (kMaxTeamShift >= 2) {
         if (S >= 4) {
 #pragma unroll
           for (int d = 0; d < 4; ++d)
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) acc[d][j] += MSDA_DPP(acc[d][j], 0x120 + 2 * KQ);
+            for (int j = 0; j < CPL; ++j) acc[j][d] += MSDA_DPP(acc[j][d], 0x120 + 2 * KQ);
         }
       }
       if (sub == S - 1) {
@@ -1190,8 +1309,8 @@ __global__ void __launch_bounds__(kTileBlock)
           float4 *dst = reinterpret_cast<float4 *>(planes + (d * NPOS + p_id) * C + k * CPL);
 #pragma unroll
           for (int h = 0; h < CPL / 4; ++h) {
-            float4 cur = make_float4(acc[d][4 * h], acc[d][4 * h + 1], acc[d][4 * h + 2],
-                                     acc[d][4 * h + 3]);
+            float4 cur = make_float4(acc[4 * h][d], acc[4 * h + 1][d], acc[4 * h + 2][d],
+                                     acc[4 * h + 3][d]);
             if (!first_of_item) {
               const float4 old = dst[h];
               cur.x += old.x;

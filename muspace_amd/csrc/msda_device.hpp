@@ -316,6 +316,7 @@ __device__ __forceinline__ float group_max_n(float v, int n) {
 // offset past the end returns zeros (hardware range check), which the row
 // kernels use for bilinear corners outside their level.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));  // an MFMA accumulator
 constexpr uint32_t kOobOffset = 0x80000000u;  // past the end of every buffer used here (< 2 GiB)
 constexpr uint32_t kBufferWord3 = 0x00020000u;  // raw, untyped 32-bit data
 
