@@ -138,8 +138,11 @@ __device__ __forceinline__ void stage_tiles(const Level *lv, int levels, int *nt
 // the tile holding (max(y0, 0), max(x0, 0)).
 template <int T>
 __device__ __forceinline__ int primary_tile(const Tap &t, int ntc, int base) {
-  const int py = t.y0 < 0 ? 0 : t.y0, px = t.x0 < 0 ? 0 : t.x0;
-  return base + (py / T) * ntc + px / T;
+  // unsigned division by the constant T (py, px >= 0): a multiply-high and
+  // a shift, without the signed form's sign fix-up
+  const unsigned py = t.y0 < 0 ? 0u : static_cast<unsigned>(t.y0);
+  const unsigned px = t.x0 < 0 ? 0u : static_cast<unsigned>(t.x0);
+  return base + static_cast<int>(py / T) * ntc + static_cast<int>(px / T);
 }
 
 // Tile geometry of slab-local tile index tl.
@@ -241,28 +244,64 @@ __global__ void __launch_bounds__(kBinBlock)
   const int lpp = 1 << p.lp_log2;
   const int total = nq * lpp;
   constexpr int U = 8;  // 16 measured slower (c2 bin_count 40.5 -> 44.6 us)
-  for (int i0 = threadIdx.x; i0 < total; i0 += kBinBlock * U) {
-    float lx[U], ly[U];
-    bool live[U];
-    int smp[U];
+  if (lpp <= kBinBlock) {
+    // a thread's samples are kBinBlock apart, a multiple of lpp: all have
+    // sample index smp = tid % lpp, so its level, level table entries and
+    // tile base are loaded once, and a sample's location is a 32-bit offset
+    // (queries of the group x floats per query) from the group's first one
+    const int smp = static_cast<int>(threadIdx.x) & (lpp - 1);
+    const bool smp_ok = smp < s.lp;
+    const int l = level_of_sample(smp_ok ? smp : 0, s);
+    const Level L = lv[l];
+    const int tnc = ntc[l], tbase = base[l];
+    const GT *loc_g =
+        loc + 2 * ((static_cast<size_t>(b * s.queries + q0) * s.heads + m) * s.lp);
+    const uint32_t q_floats = 2u * static_cast<uint32_t>(s.heads * s.lp);
+    for (int i0 = threadIdx.x; i0 < total; i0 += kBinBlock * U) {
+      float lx[U], ly[U];
+      bool live[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + u * kBinBlock;
-      const int q = q0 + (i >> p.lp_log2);
-      smp[u] = i & (lpp - 1);
-      live[u] = i < total && smp[u] < s.lp;
-      const size_t o =
-          live[u] ? (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp[u] : 0;
-      lx[u] = load_nt(&loc[2 * o]);
-      ly[u] = load_nt(&loc[2 * o + 1]);
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kBinBlock;
+        live[u] = i < total && smp_ok;
+        const uint32_t off = live[u] ? static_cast<uint32_t>(i >> p.lp_log2) * q_floats +
+                                           2u * static_cast<uint32_t>(smp)
+                                     : 0u;
+        lx[u] = load_nt(&loc_g[off]);
+        ly[u] = load_nt(&loc_g[off + 1]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kBinBlock;
+        const Tap t = make_tap(lx[u], ly[u], L, live[u]);
+        const int row = (i >> p.lp_log2) >> cq_log2;  // chunk of the group
+        if (t.in) atomicAdd(&hist[row * nt + primary_tile<T>(t, tnc, tbase)], 1u);
+      }
     }
+  } else {
+    for (int i0 = threadIdx.x; i0 < total; i0 += kBinBlock * U) {
+      float lx[U], ly[U];
+      bool live[U];
+      int smp[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + u * kBinBlock;
-      const int l = level_of_sample(live[u] ? smp[u] : 0, s);
-      const Tap t = make_tap(lx[u], ly[u], lv[l], live[u]);
-      const int row = (i >> p.lp_log2) >> cq_log2;  // chunk of the group
-      if (t.in) atomicAdd(&hist[row * nt + primary_tile<T>(t, ntc[l], base[l])], 1u);
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kBinBlock;
+        const int q = q0 + (i >> p.lp_log2);
+        smp[u] = i & (lpp - 1);
+        live[u] = i < total && smp[u] < s.lp;
+        const size_t o =
+            live[u] ? (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp[u] : 0;
+        lx[u] = load_nt(&loc[2 * o]);
+        ly[u] = load_nt(&loc[2 * o + 1]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kBinBlock;
+        const int l = level_of_sample(live[u] ? smp[u] : 0, s);
+        const Tap t = make_tap(lx[u], ly[u], lv[l], live[u]);
+        const int row = (i >> p.lp_log2) >> cq_log2;  // chunk of the group
+        if (t.in) atomicAdd(&hist[row * nt + primary_tile<T>(t, ntc[l], base[l])], 1u);
+      }
     }
   }
 
