@@ -706,6 +706,11 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=100)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    parser.add_argument("--value-dtype", default="float32",
+                        choices=["float32", "bfloat16", "float16"],
+                        help="storage type of value and grad_output in the main step "
+                             "(locations and weights stay float32); c4 is quoted in the "
+                             "16-bit types")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extra-configs", action="store_true")
     parser.add_argument("--repeats", type=int, default=5,
@@ -777,11 +782,13 @@ def main() -> int:
         return 0
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
-    print(f"[bench] inputs for {cfg.name}", file=sys.stderr, flush=True)
-    step = Step(lib, cfg, torch.float32, torch.float32, dev,
+    vdt = getattr(torch, args.value_dtype)
+    vname = {"float32": "float", "bfloat16": "bf16_t", "float16": "__half"}[args.value_dtype]
+    print(f"[bench] inputs for {cfg.name} {args.value_dtype}", file=sys.stderr, flush=True)
+    step = Step(lib, cfg, vdt, torch.float32, dev,
                 binning="serial" if args.serial_backward else "fused")
     res = time_steps(step, args.steps, args.warmup, repeats=args.repeats)
-    fwd_b, bwd_b = algorithmic_bytes(cfg)
+    fwd_b, bwd_b = algorithmic_bytes(cfg, vdt)
     gbps = (fwd_b + bwd_b) / (res["ms_per_step"] * 1e-3) / 1e9
     print(f"[bench] {cfg.name}: {res}", file=sys.stderr, flush=True)
     del step
@@ -850,7 +857,9 @@ def main() -> int:
         if "c0-float32-forward" in extra:
             extra["c0-float32-forward"]["cpu_fwd_us"] = round(cpu["rows"]["c0"]["ms"] * 1e3, 1)
 
-    rest_b = backward_rest_bytes(cfg)
+    rest_b = backward_rest_bytes(cfg, vdt)
+    # the stored traffic summary is the c2 float32 step's
+    headline = cfg.name == "c2" and vdt == torch.float32
     rest_achieved = rest_b / (res["rest_ms"] * 1e-3) / 1e9
     line = {
         "metric": METRIC,
@@ -867,10 +876,11 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": {"float32": "f32", "bfloat16": "bf16", "float16": "f16"}[args.value_dtype],
         "data": "synthetic (seed 2333; value, grad ~ N(0,1), locations ~ U(0,1), softmax weights)",
         "config": {
-            "workload": f"{cfg.name}: BEVFormer SCA MSDA fwd+bwd, bs*cams {cfg.batch}, "
+            "workload": f"{cfg.name}: {cfg.description}, MSDA fwd+bwd, {args.value_dtype} "
+                        f"value, batch {cfg.batch}, "
                         f"nq {cfg.queries}, heads {cfg.heads}, head_dim {cfg.channels}, "
                         f"levels {list(cfg.levels)}, points {cfg.points}",
             "us_per_call": round(res["ms_per_step"] * 1e3, 1),
@@ -879,21 +889,21 @@ def main() -> int:
             "bin_us": round(res["bin_ms"] * 1e3, 1),
             "rest_us": round(res["rest_ms"] * 1e3, 1),
             "alloc_us": round(res["zero_ms"] * 1e3, 1),
-            "forward_kernel_stores_records": fused_binning(lib, cfg, torch.float32),
+            "forward_kernel_stores_records": fused_binning(lib, cfg, vdt),
             "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
             "algorithmic_bytes": {"fwd": fwd_b, "bwd": bwd_b},
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "msda_tile_backward<float,32> (ms_deform_attn_backward_rest: "
+            "kernel": f"msda_tile_backward<{vname},32> (ms_deform_attn_backward_rest: "
                       f"{rest_b:,} algorithmic bytes = value, grad_output, grad_value, "
                       "grad_sampling_locations, grad_attention_weights once)",
             "achieved": round(rest_achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(rest_achieved / HBM_PEAK_GBPS, 4),
-            "traffic": read_traffic(),
-            "traffic_source": str(TRAFFIC_FILE.relative_to(ROOT)),
+            "traffic": read_traffic() if headline else None,
+            "traffic_source": str(TRAFFIC_FILE.relative_to(ROOT)) if headline else None,
         },
         "cpu_baseline": cpu,
         "other_configs": extra,
