@@ -109,10 +109,16 @@ template <> struct TileCfg<__half, 16> : TileCfg<bf16_t, 16> {};
 template <> struct TileCfg<__half, 32> : TileCfg<bf16_t, 32> {};
 template <> struct TileCfg<__half, 64> : TileCfg<bf16_t, 64> {};
 
+// Padding after each value-tile cell in LDS (one 16-byte unit): a cell's row
+// is 128 bytes in fp32 (64 in 16-bit), a multiple of the bank width, so
+// without it the owner groups' reads of 16 different cells started on two
+// bank offsets only.
+constexpr int kVtPad = 16;
+
 template <typename VT, int C>
 __host__ __device__ constexpr size_t tile_lds_bytes() {
   constexpr int T = TileCfg<VT, C>::T, K = TileCfg<VT, C>::K, NPOS = (T + 1) * (T + 1);
-  return static_cast<size_t>(NPOS + 1) * C * sizeof(VT) +  // value tile + halo, zero row
+  return static_cast<size_t>(NPOS + 1) * (C * sizeof(VT) + kVtPad) +  // value tile, zero row
          static_cast<size_t>(4 * NPOS) * C * 4 +           // corner planes
          static_cast<size_t>(K) * 16 +                     // sorted records
          static_cast<size_t>(4 * NPOS) * 4 +               // position count, offset, rank table
@@ -818,8 +824,9 @@ __global__ void __launch_bounds__(kTileBlock)
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
   __shared__ int team_shift_s;  // log2 of the owner team size of the current batch
   extern __shared__ __align__(16) unsigned char lds[];
-  VT *vt = reinterpret_cast<VT *>(lds);  // NPOS cells + one zero row
-  float *planes = reinterpret_cast<float *>(lds + static_cast<size_t>(NPOS + 1) * C * VB);
+  constexpr int CS = C + kVtPad / VB;  // elements per value-tile cell, with its padding
+  VT *vt = reinterpret_cast<VT *>(lds);  // NPOS cells + one zero row, CS elements apart
+  float *planes = reinterpret_cast<float *>(lds + static_cast<size_t>(NPOS + 1) * CS * VB);
   uint4 *stash = reinterpret_cast<uint4 *>(planes + 4 * NPOS * C);
   uint32_t *pcount = reinterpret_cast<uint32_t *>(stash + K);
   uint32_t *poff = pcount + NPOS;
@@ -955,7 +962,8 @@ __global__ void __launch_bounds__(kTileBlock)
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
       const int unit = tid + v * kTileBlock;
-      if (unit < NPOS * UPV) reinterpret_cast<uint4 *>(vt)[unit] = vt_next[v];
+      // unit kk of cell c -> 16-byte slot c * (UPV + 1) + kk (the padding)
+      if (unit < NPOS * UPV) reinterpret_cast<uint4 *>(vt)[unit + unit / UPV] = vt_next[v];
     }
   };
   // cell sums of a finished item's corner planes to grad_value: cell (r, c)
@@ -1038,7 +1046,7 @@ __global__ void __launch_bounds__(kTileBlock)
   for (int u = 0; u < RPT; ++u) r_cur[u] = load_record(c0, u);
   load_value_tile(c0.d, true);
   store_value_tile();
-  if (tid < UPV) reinterpret_cast<uint4 *>(vt + NPOS * C)[tid] = make_uint4(0u, 0u, 0u, 0u);
+  if (tid < UPV) reinterpret_cast<uint4 *>(vt + NPOS * CS)[tid] = make_uint4(0u, 0u, 0u, 0u);
   if (tid < NPOS) pcount[tid] = 0;
   if (tid < kWave) bucket[tid] = 0;
   __syncthreads();
@@ -1228,7 +1236,7 @@ __global__ void __launch_bounds__(kTileBlock)
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
           const int cy = py + (d >> 1), cx = px + (d & 1);
-          lds_row8(vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * C : NPOS * C) + k * CPL, v[d]);
+          lds_row8(vt + ((cy >= 0 && cx >= 0) ? (cy * TV + cx) * CS : NPOS * CS) + k * CPL, v[d]);
         }
         // One record: its four corner dot products (stored over its stash
         // slot) and, except where the MFMA sums run, its corner sums. With
