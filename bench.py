@@ -536,7 +536,8 @@ def cpu_baseline() -> dict:
 
 
 def time_forward_only(lib, name: str) -> dict:
-    """A forward-only config (c0) through the C-ABI forward, reference protocol."""
+    """A config's forward alone (c0, whose case is forward-only; c2 without a
+    gradient graph) through the C-ABI forward, reference protocol."""
     cfg = CONFIGS[name]
     t = make_inputs(cfg, device="cuda", with_grad_output=False)
     out = torch.empty((cfg.batch, cfg.queries, cfg.heads * cfg.channels), device="cuda")
@@ -834,6 +835,11 @@ def main() -> int:
         torch.cuda.empty_cache()
         print("[bench] extra c0 forward", file=sys.stderr, flush=True)
         extra["c0-float32-forward"] = time_forward_only(lib, "c0")
+        torch.cuda.empty_cache()
+        # the forward alone (no gradient graph: no binning), beside the main
+        # step's forward call, which also bins the samples for the backward
+        print("[bench] extra c2 forward only", file=sys.stderr, flush=True)
+        extra["c2-float32-forward-only"] = time_forward_only(lib, "c2")
         torch.cuda.empty_cache()
         for dtype in (torch.float32, torch.bfloat16):
             label = str(dtype).replace("torch.", "")
