@@ -153,6 +153,82 @@ class Step:
         mark("rest1", main)
 
 
+PARITY_QUERIES = 48  # queries per batch entry checked against the oracle
+
+
+def check_step_parity(step: Step, cfg, value_dtype) -> dict:
+    """The timed step's results, from one untimed run of the same launches on
+    the same inputs, against the oracle (oracle/msda_torch.py, the CPU
+    restatement of the reference's PyTorch path, as the checker only).
+
+    On a seeded subset of PARITY_QUERIES queries (every batch entry) the
+    output and the location and weight gradients depend only on those
+    queries, so the oracle on the subset gives their exact values. grad_value
+    sums over all queries; it is checked at full size through the adjoint
+    identities <grad_out, out> = <value, grad_value> = <attn, grad_attn>
+    (MSDA is linear in value and in the attention weights), and every
+    gradient element must have been written (finite). Tolerances are the
+    north star's: float32 output 1e-5 and gradients 1e-4, 16-bit storage
+    1e-2 (|a - e| <= tol + tol |e|); adjoint identities 1e-5 (float32) and
+    3e-3 (16-bit) of sum |grad_out * out|."""
+    from oracle import msda_torch
+
+    bufs = step.alloc()
+    if step.binning == "fused":
+        out = step.forward_bin(bufs)
+    else:
+        saved, step.side = step.side, torch.cuda.current_stream()
+        step.bin(bufs)
+        step.side = saved
+        out = step.forward()
+    step.rest(bufs)
+    torch.cuda.synchronize()
+    gv, gl, ga, _ = bufs
+
+    g = torch.Generator().manual_seed(7)
+    idx = torch.randperm(cfg.queries, generator=g)[:PARITY_QUERIES].sort().values
+    idx_dev = idx.to(out.device)
+    value = step.value.float().cpu()
+    loc = step.loc[:, idx_dev].float().cpu()
+    attn = step.attn[:, idx_dev].float().cpu()
+    grad = step.grad[:, idx_dev].float().cpu()
+    o_out, _, o_gl, o_ga = msda_torch.msda_forward_backward(value, step.shapes.cpu(), loc, attn,
+                                                            grad)
+    ftol, btol = (1e-5, 1e-4) if value_dtype == torch.float32 else (1e-2, 1e-2)
+
+    def worst(actual, expected, tol):
+        """max of |a - e| / (tol + tol |e|): at most 1 passes"""
+        a, e = actual.double().cpu(), expected.double()
+        return float(((a - e).abs() / (tol + tol * e.abs())).max())
+
+    ratios = {
+        "output": worst(out[:, idx_dev], o_out, ftol),
+        "grad_sampling_locations": worst(gl[:, idx_dev], o_gl, btol),
+        "grad_attention_weights": worst(ga[:, idx_dev], o_ga, btol),
+    }
+    written = bool(torch.isfinite(gv).all() and torch.isfinite(gl).all()
+                   and torch.isfinite(ga).all())
+    lhs = float((out.double() * step.grad.double()).sum())
+    scale = float((out.double().abs() * step.grad.double().abs()).sum())
+    rel = 1e-5 if value_dtype == torch.float32 else 3e-3
+    adj_v = abs(lhs - float((step.value.double() * gv.double()).sum())) / (rel * scale)
+    adj_a = abs(lhs - float((step.attn.double() * ga.double()).sum())) / (rel * scale)
+    ratios["adjoint_value_grad_value"] = adj_v
+    ratios["adjoint_attn_grad_attn"] = adj_a
+    ok = written and all(r <= 1.0 for r in ratios.values())
+    del bufs, out
+    return {
+        "ok": ok,
+        "checked": f"one run of the timed step's launches, before timing: output, "
+                   f"grad_sampling_locations and grad_attention_weights on {PARITY_QUERIES} "
+                   f"seeded queries x {cfg.batch} batch entries against oracle/msda_torch.py; "
+                   f"grad_value through the adjoint identities at full size",
+        "tolerance": {"forward": ftol, "backward": btol, "adjoint_rel": rel},
+        "worst_error_over_tolerance": {k: round(v, 4) for k, v in ratios.items()},
+        "all_gradients_written": written,
+    }
+
+
 def fused_binning(lib, cfg, value_dtype) -> bool:
     """Whether ms_deform_attn_forward_bin stores the backward's records from
     the forward kernel at this config (else the plain forward and the
@@ -788,6 +864,11 @@ def main() -> int:
     print(f"[bench] inputs for {cfg.name} {args.value_dtype}", file=sys.stderr, flush=True)
     step = Step(lib, cfg, vdt, torch.float32, dev,
                 binning="serial" if args.serial_backward else "fused")
+    print(f"[bench] parity of the timed step ({cfg.name})", file=sys.stderr, flush=True)
+    parity = check_step_parity(step, cfg, vdt)
+    print(f"[bench] parity: {parity['ok']} {parity['worst_error_over_tolerance']}",
+          file=sys.stderr, flush=True)
+    torch.cuda.empty_cache()
     res = time_steps(step, args.steps, args.warmup, repeats=args.repeats)
     fwd_b, bwd_b = algorithmic_bytes(cfg, vdt)
     gbps = (fwd_b + bwd_b) / (res["ms_per_step"] * 1e-3) / 1e9
@@ -911,10 +992,15 @@ def main() -> int:
             "traffic": read_traffic() if headline else None,
             "traffic_source": str(TRAFFIC_FILE.relative_to(ROOT)) if headline else None,
         },
+        "parity": parity,
         "cpu_baseline": cpu,
         "other_configs": extra,
     }
     print(json.dumps(line, ensure_ascii=False), flush=True)
+    if not parity["ok"]:
+        print("[bench] the timed step's results do not match the oracle", file=sys.stderr,
+              flush=True)
+        return 1
     return 0
 
 

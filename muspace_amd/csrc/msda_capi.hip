@@ -1035,11 +1035,15 @@ int64_t noalloc_batch_step(const msda::Shape &s, int value_dtype, size_t *one_en
     if (!plan_tile_workspace(sc, value_dtype, w)) return 0;
     if (nb == 1) *one_entry_bytes = w.bytes;
     if (w.bytes <= kNoAllocScratchBytes) return nb;
-    // the workspace grows about linearly with the batch entries
+    // the workspace grows about linearly with the batch entries; the next
+    // count is at least 1, so that one entry's size is always planned (and
+    // reported when even that does not fit)
     const int64_t scaled = static_cast<int64_t>(
         static_cast<double>(nb) * static_cast<double>(kNoAllocScratchBytes) /
         static_cast<double>(w.bytes));
-    nb = scaled < nb ? scaled : nb - 1;
+    const int64_t next = scaled < nb ? scaled : nb - 1;
+    if (nb == 1) break;
+    nb = next < 1 ? 1 : next;
   }
   return 0;
 }

@@ -461,7 +461,8 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
   };
 
   // the start of step st: its unit's epilogue data; kSoftmax with a unit of
-  // several steps: rescale to the step's running max
+  // several steps: rescale to the step's running max, which tap(st) wrote
+  // (so tap(st) must come first)
   auto begin_step = [&](int st) {
     if (st % chunks == 0) out.fetch_count(tk_cur, ou.b, s);
     if constexpr (kSoftmax) {
@@ -526,8 +527,10 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
     // c1 179 -> 201 us, c3 133 -> 137 us)
     (void)raw1;
     for (int st = 0; st < steps; ++st) {
-      begin_step(st);
+      // the tap first: with kSoftmax it writes the step's rescale, which
+      // begin_step applies
       tap(st);
+      begin_step(st);
       issue(st, 0, raw0);
       load_geometry(st + 1);
       consume(st, 0, raw0);

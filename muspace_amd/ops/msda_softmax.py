@@ -62,7 +62,13 @@ def _start_binning(ext, value, spatial, starts, sampling, logits, im2col_step):
                                      value, sampling, logits)
     if release is None:
         return None
-    workspace = ext.backward_softmax_workspace(value, sampling)
+    try:
+        workspace = ext.backward_softmax_workspace(value, sampling)
+    except BaseException:
+        release()  # nothing was allocated: the reservation goes back now
+        raise
+    # from here on the workspace's finalizer returns the reservation, also
+    # when an allocation below raises and drops the workspace
     weakref.finalize(workspace, release)
     device = value.device
     grads = (

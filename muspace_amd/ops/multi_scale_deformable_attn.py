@@ -239,7 +239,13 @@ def _binning_buffers(ext, value, sampling, attn):
     release = _reserve_early_buffers(nbytes, value, sampling, attn)
     if release is None:
         return None
-    workspace = ext.backward_workspace(value, sampling)
+    try:
+        workspace = ext.backward_workspace(value, sampling)
+    except BaseException:
+        release()  # nothing was allocated: the reservation goes back now
+        raise
+    # from here on the workspace's finalizer returns the reservation, also
+    # when an allocation below raises and drops the workspace
     weakref.finalize(workspace, release)
     device = value.device
     grads = (

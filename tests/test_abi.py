@@ -96,13 +96,19 @@ def test_backward_validation_fails_before_any_launch(native_lib):
 
 def test_noalloc_backward_rejects_an_entry_larger_than_its_scratch(native_lib):
     """One batch entry of 8 heads x 100000 queries x 32 samples needs about
-    420 MB of tile scratch, more than the 64 MiB array: MUSPACE_ERANGE before
+    630 MB of tile scratch, more than the 64 MiB array: MUSPACE_ERANGE before
     anything runs (the pointers are stand-ins; nothing may read them)."""
     fn = native_lib.raw("ms_deform_attn_backward_noalloc")
     args = [1, 0, 1, 1, 1, 1, 0, 1, 1, 1, 1,
             2, 30825, 8, 32, 4, 100000, 8, 64, None]
     assert fn(*args) == 2  # MUSPACE_ERANGE
-    assert "needs" in native_lib.last_error() and "scratch" in native_lib.last_error()
+    msg = native_lib.last_error()
+    assert "needs" in msg and "scratch" in msg
+    # two entries' workspace is far past the array, so the planner steps down
+    # to one entry, and reports that entry's real size
+    needed = int(re.search(r"needs (\d+) bytes", msg).group(1))
+    size = native_lib.raw("ms_deform_attn_backward_workspace_size")
+    assert needed == size(0, 1, 30825, 8, 32, 4, 100000, 8) > (64 << 20), msg
     args[1:2] = [9]  # a bad dtype is still MUSPACE_EINVAL, first
     assert fn(*args) == 1
 

@@ -385,13 +385,14 @@ def test_full_config_parity(native_lib, name, value_dtype, geometry_dtype):
     _check_full_config(native_lib, name, value_dtype, geometry_dtype, fused=False)
 
 
-# The fused forward + binning at full size: the direct gradient writes (c2,
-# c3), the records-plus-gather path (c1, c4) and 16-bit values (c4).
+# The fused forward + binning at full size, at every config the bench times
+# through it: float32 (c1, c2, c3) and both 16-bit value types (c4).
 FULL_FUSED = [
     ("c1", torch.float32, torch.float32),
     ("c2", torch.float32, torch.float32),
     ("c3", torch.float32, torch.float32),
     ("c4", torch.bfloat16, torch.float32),
+    ("c4", torch.float16, torch.float32),
 ]
 
 

@@ -99,6 +99,18 @@ def test_16bit_storage_matches_the_oracle(vdt, gdt):
                 _oracle(value, shapes, loc, logits, grad, vdt, gdt), 2e-2, 2e-2)
 
 
+@pytest.mark.parametrize("vdt", [torch.bfloat16, torch.float16])
+def test_16bit_c16_two_steps_per_unit(vdt):
+    """16-bit values with C = 16 run two lanes per row (two samples per lane
+    group and step), so L*P = 128 takes two steps per unit in the one-stage
+    loop: the second step's online-softmax rescale must be the one its own
+    tap computed (applying it before the tap used the step-before-last's)."""
+    case = _case(8, channels=16, points=32)
+    value, shapes, starts, loc, logits, grad = case
+    _assert_all(_native(*case, vdt=vdt, gdt=torch.float32),
+                _oracle(value, shapes, loc, logits, grad, vdt, torch.float32), 2e-2, 2e-2)
+
+
 def test_minus_infinity_logits():
     """Masked samples get weight zero; a unit whose logits are all -inf gives
     NaN, as torch.softmax does (its output row and its logit gradients)."""

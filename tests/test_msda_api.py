@@ -253,3 +253,37 @@ def test_compat_signature_derives_level_start_index():
     value, shapes, _, loc, attn = _fixture(levels=((1, 2), (2, 3), (1, 1)), points=2)
     out = multi_scale_deformable_attn_pytorch_compat(value, shapes, loc, attn)
     torch.testing.assert_close(out, msda_torch.msda_forward(value, shapes, loc, attn))
+
+
+@pytest.mark.parametrize("which", ["msda", "softmax"])
+def test_early_binning_reservation_returns_when_the_workspace_allocation_fails(
+        which, monkeypatch):
+    """A failed workspace allocation (out of memory) gives its early-binning
+    reservation back at once; otherwise every such failure would shrink the
+    device's budget for good, until early binning silently stopped."""
+    msda_module = import_module("muspace_amd.ops.multi_scale_deformable_attn")
+    softmax_module = import_module("muspace_amd.ops.msda_softmax")
+    budget = msda_module.BinningBudget(limit_of=lambda index: 1 << 40)
+    monkeypatch.setattr(msda_module, "binning_budget", budget)
+    monkeypatch.setattr(msda_module, "_device_index", lambda device: 0)
+
+    class FailingExtension:
+        def backward_workspace_bytes(self, value, sampling):
+            return 1 << 20
+
+        backward_softmax_workspace_bytes = backward_workspace_bytes
+
+        def backward_workspace(self, value, sampling):
+            raise MemoryError("out of device memory")
+
+        backward_softmax_workspace = backward_workspace
+
+    value = torch.zeros(1, 4, 2, 8)
+    sampling = torch.zeros(1, 3, 2, 1, 2, 2)
+    attn = torch.zeros(1, 3, 2, 1, 2)
+    with pytest.raises(MemoryError):
+        if which == "msda":
+            msda_module._binning_buffers(FailingExtension(), value, sampling, attn)
+        else:
+            softmax_module._start_binning(FailingExtension(), value, None, None, sampling, attn, 64)
+    assert budget.held(0) == 0

@@ -5,6 +5,9 @@ tolerance (1e-4; tile-boundary sums are added atomically, in no fixed order).
 The first call has the c2 shape, whose six batch entries do not fit the fixed
 scratch together, so it runs in several passes over the batch; the second is
 small enough for one pass and must not see anything the first left behind.
+A third case stores value, grad_output and the geometry in bfloat16 and has a
+batch of five whose passes hold three entries and then two, so the per-pass
+offsets are checked at 16-bit element sizes and for a short last pass.
 """
 
 from __future__ import annotations
@@ -15,6 +18,7 @@ import pytest
 import torch
 
 from conftest import gpu_available
+from muspace_amd.runtime.native import DTYPE_BF16, DTYPE_F16, DTYPE_F32
 from muspace_amd.workloads import CONFIGS, make_inputs
 
 pytestmark = [
@@ -48,15 +52,18 @@ def _device(t):
     return {k: v.to(DEV).contiguous() for k, v in t.items()}
 
 
+_CODES = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+
+
 def _raw_noalloc(lib, t, grads):
     """ms_deform_attn_backward_noalloc through the bare C entry point."""
     value, loc = t["value"], t["sampling_locations"]
     batch, spatial, heads, channels = value.shape
     _, queries, _, levels, points, _ = loc.shape
     fn = lib.raw("ms_deform_attn_backward_noalloc")
-    rc = fn(value.data_ptr(), 0, t["spatial_shapes"].data_ptr(),
+    rc = fn(value.data_ptr(), _CODES[value.dtype], t["spatial_shapes"].data_ptr(),
             t["level_start_index"].data_ptr(), loc.data_ptr(),
-            t["attention_weights"].data_ptr(), 0, t["grad_output"].data_ptr(),
+            t["attention_weights"].data_ptr(), _CODES[loc.dtype], t["grad_output"].data_ptr(),
             grads[0].data_ptr(), grads[1].data_ptr(), grads[2].data_ptr(),
             batch, spatial, heads, channels, levels, queries, points, 64,
             torch.cuda.current_stream().cuda_stream)
@@ -64,7 +71,7 @@ def _raw_noalloc(lib, t, grads):
 
 
 def _poisoned(t):
-    return tuple(torch.full(t[k].shape, float("nan"), device=DEV)
+    return tuple(torch.full(t[k].shape, float("nan"), device=DEV, dtype=torch.float32)
                  for k in ("value", "sampling_locations", "attention_weights"))
 
 
@@ -95,3 +102,34 @@ def test_noalloc_backward_matches_the_allocating_entry_twice(native_lib):
     small = _device(_small_inputs())
     print("[no-alloc] second, smaller call", flush=True)
     _check(native_lib, small)
+
+
+def test_noalloc_backward_16bit_storage_with_a_short_last_pass(native_lib):
+    """bfloat16 value, grad_output, locations and weights; five batch entries
+    of 4000 queries at the c2 levels: three entries' workspace fits the
+    scratch and four do not, so the passes hold three entries and then two."""
+    cfg = CONFIGS["c2"]
+    batch, queries = 5, 4000
+    size = native_lib.raw("ms_deform_attn_backward_workspace_size")
+    per = [size(DTYPE_BF16, n, cfg.spatial_size, cfg.heads, cfg.channels, cfg.num_levels,
+                queries, cfg.points) for n in (3, 4)]
+    assert per[0] <= SCRATCH < per[1]
+    g = torch.Generator().manual_seed(5)
+    levels = cfg.levels
+    logits = torch.randn(batch, queries, cfg.heads, cfg.num_levels * cfg.points, generator=g)
+    starts = [0]
+    for h, w in levels[:-1]:
+        starts.append(starts[-1] + h * w)
+    t = {
+        "value": torch.randn(batch, cfg.spatial_size, cfg.heads, cfg.channels, generator=g),
+        "spatial_shapes": torch.tensor(levels, dtype=torch.int64),
+        "level_start_index": torch.tensor(starts, dtype=torch.int64),
+        "sampling_locations": torch.rand(batch, queries, cfg.heads, cfg.num_levels, cfg.points,
+                                         2, generator=g),
+        "attention_weights": torch.softmax(logits, -1).view(batch, queries, cfg.heads,
+                                                            cfg.num_levels, cfg.points),
+        "grad_output": torch.randn(batch, queries, cfg.heads * cfg.channels, generator=g),
+    }
+    t = {k: (v.to(torch.bfloat16) if v.is_floating_point() else v) for k, v in t.items()}
+    print(f"[no-alloc] bf16: batch {batch} x {queries} queries, passes of 3 + 2", flush=True)
+    _check(native_lib, _device(t))
