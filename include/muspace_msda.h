@@ -56,7 +56,7 @@
 extern "C" {
 #endif
 
-#define MUSPACE_MSDA_ABI_VERSION 5
+#define MUSPACE_MSDA_ABI_VERSION 6
 
 /* the library is built with -fvisibility=hidden; only these symbols export */
 #if defined(__GNUC__)
@@ -315,6 +315,34 @@ MUSPACE_API int ms_deform_attn_backward_softmax_rest(
     int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
     int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
     size_t workspace_bytes, void *stream);
+
+/* ms_deform_attn_forward_softmax followed by ms_deform_attn_backward_softmax_bin
+ * on the same arguments, workspace (as sized above) and stream, in one call:
+ * the output plus the probabilities and the binned workspace that
+ * ms_deform_attn_backward_softmax_rest then consumes. Where the tile path
+ * applies and each unit's L*P logits fit one step of the forward row kernel,
+ * the softmax-fused forward kernel itself writes the probabilities and stores
+ * the backward's records (weighted by the probabilities), as
+ * ms_deform_attn_forward_bin does; elsewhere it makes exactly those two calls.
+ * Same contract as the two calls. No reference counterpart (the reference's
+ * callers apply the softmax in torch before its forward). */
+MUSPACE_API int ms_deform_attn_forward_softmax_bin(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_logits, int geometry_dtype, void *output, float *grad_value,
+    float *grad_sampling_locations, float *grad_attention_logits, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream);
+
+/* 1 if ms_deform_attn_forward_softmax_bin (aligned tensors, a workspace as
+ * above) fuses the probabilities and the record stores into the forward kernel
+ * for these dims; 0 if it makes the two calls. No reference counterpart. */
+MUSPACE_API int ms_deform_attn_forward_softmax_bin_fused(int value_dtype, int64_t batch,
+                                                         int64_t spatial_size,
+                                                         int64_t num_heads, int64_t channels,
+                                                         int64_t num_levels, int64_t num_query,
+                                                         int64_t num_point);
 
 /* Both parts in one call with stream-ordered scratch (MUSPACE_ENOMEM if it
  * cannot be allocated). */

@@ -620,7 +620,8 @@ int tile_grid() {
 // The forward row kernel's units (queries of one slab) and tap slots per
 // block: the query chunk of the binning fused into the forward. False where
 // no row kernel serves the channel count.
-bool fwd_bin_chunk(const msda::Shape &s, int value_dtype, int &units, int &slots) {
+bool fwd_bin_chunk(const msda::Shape &s, int value_dtype, int &units, int &slots,
+                   int *unit_steps = nullptr) {
   if (s.channels != 16 && s.channels != 32 && s.channels != 64) return false;
   const int vb = value_dtype == MUSPACE_DTYPE_F32 ? 4 : 2;
   const int kq = s.channels / (16 / vb);
@@ -630,6 +631,7 @@ bool fwd_bin_chunk(const msda::Shape &s, int value_dtype, int &units, int &slots
   const int waves = msda::kBlock / msda::kWave;
   units = waves * L.plan.iters * (ng / gu);
   slots = waves * L.plan.iters * lchunks * ng * L.ns;  // ng * ns <= 64 taps per step
+  if (unit_steps) *unit_steps = lchunks;
   return units > 0;
 }
 
@@ -795,28 +797,35 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
 // which the fused forward measured slower to store than bin_scatter does),
 // within the block's tap slots and its LDS budget. units, slots: the
 // forward block's queries and tap slots.
+// softmax: the forward takes logits (msda_forward_softmax_bin_rows), which
+// needs units of one step each, so that a sample's probability is final when
+// its tap is computed.
 bool fwd_bin_fuses(const msda::Shape &s, int value_dtype, const TileWorkspace &w, int &units,
-                   int &slots) {
+                   int &slots, bool softmax = false) {
   if (!w.plan.direct) return false;
-  if (!fwd_bin_chunk(s, value_dtype, units, slots)) return false;
+  int unit_steps = 0;
+  if (!fwd_bin_chunk(s, value_dtype, units, slots, &unit_steps)) return false;
+  if (softmax && unit_steps != 1) return false;
   return slots <= msda::kFwdBinSlots &&
          msda::fwd_bin_lds_bytes(slots, w.plan.tile_bound) <= msda::kFwdBinDynLds;
 }
 
 // The forward with the backward's binning fused in (msda_forward_bin.hpp):
 // bin_count and bin_scan over the forward blocks' query chunks, then the
-// forward row kernel, which also stores every chunk's records. Launches
-// nothing and returns false where that does not apply.
+// forward row kernel, which also stores every chunk's records. With `probs`
+// non-null, `attn` holds logits: the kernel is the softmax-fused forward,
+// which also writes every sample's probability (GT) to `probs` and records
+// it. Launches nothing and returns false where that does not apply.
 template <typename VT, typename GT, int C>
 bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const int64_t *starts,
                               const void *loc, const void *attn, void *out, float *gv, float *gl,
                               float *ga, const msda::Shape &s, const TileWorkspace &w,
-                              void *workspace, hipStream_t st) {
+                              void *workspace, hipStream_t st, void *probs = nullptr) {
   constexpr int T = msda::TileCfg<VT, C>::T;
   constexpr int value_dtype = std::is_same<VT, float>::value ? MUSPACE_DTYPE_F32
                                                              : MUSPACE_DTYPE_F16;
   int units = 0, slots = 0;
-  if (!fwd_bin_fuses(s, value_dtype, w, units, slots)) return false;
+  if (!fwd_bin_fuses(s, value_dtype, w, units, slots, probs != nullptr)) return false;
   unsigned char *ws = static_cast<unsigned char *>(workspace);
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + w.counts);
   uint32_t *tile_start = reinterpret_cast<uint32_t *>(ws + w.tile_start);
@@ -850,11 +859,12 @@ bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const in
                                                                    counts, item_total, gv);
   msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
       shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
-  const msda::FwdBinArgs args{counts, zero_tiles, records, gl, ga, gv, p, slots};
+  const msda::FwdBinArgs args{counts, zero_tiles, records, gl, ga, gv, p, slots, probs};
   const size_t lds = msda::fwd_bin_lds_bytes(slots, p.tile_bound);
   const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
   forward_rows_ns<VT, C>(s, [&](auto ns, const Launch &L) {
-    auto k = msda::msda_forward_bin_rows<VT, GT, C, decltype(ns)::value, T>;
+    auto k = probs ? msda::msda_forward_softmax_bin_rows<VT, GT, C, decltype(ns)::value, T>
+                   : msda::msda_forward_bin_rows<VT, GT, C, decltype(ns)::value, T>;
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     k<<<bm * p.chunks, msda::kBlock, lds, st>>>(static_cast<const VT *>(value), vbytes, shapes,
@@ -868,7 +878,7 @@ template <typename VT, typename GT>
 bool launch_forward_bin(const void *value, const int64_t *shapes, const int64_t *starts,
                         const void *loc, const void *attn, void *out, float *gv, float *gl,
                         float *ga, const msda::Shape &s, void *workspace, size_t workspace_bytes,
-                        hipStream_t st) {
+                        hipStream_t st, void *probs = nullptr) {
   constexpr int value_dtype = std::is_same<VT, float>::value ? MUSPACE_DTYPE_F32
                                                              : MUSPACE_DTYPE_F16;
   TileWorkspace w;
@@ -879,13 +889,13 @@ bool launch_forward_bin(const void *value, const int64_t *shapes, const int64_t 
   switch (s.channels) {
     case 16:
       return launch_forward_bin_tiles<VT, GT, 16>(value, shapes, starts, loc, attn, out, gv, gl,
-                                                  ga, s, w, workspace, st);
+                                                  ga, s, w, workspace, st, probs);
     case 32:
       return launch_forward_bin_tiles<VT, GT, 32>(value, shapes, starts, loc, attn, out, gv, gl,
-                                                  ga, s, w, workspace, st);
+                                                  ga, s, w, workspace, st, probs);
     case 64:
       return launch_forward_bin_tiles<VT, GT, 64>(value, shapes, starts, loc, attn, out, gv, gl,
-                                                  ga, s, w, workspace, st);
+                                                  ga, s, w, workspace, st, probs);
     default:
       return false;
   }
@@ -1544,6 +1554,77 @@ int ms_deform_attn_backward_softmax_bin(
                        grad_output, grad_value, grad_sampling_locations, grad_attention_logits,
                        a, workspace, workspace_bytes, static_cast<hipStream_t>(stream),
                        Phase::kBin, true);
+}
+
+int ms_deform_attn_forward_softmax_bin(
+    const void *value, int value_dtype, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_locations,
+    const void *attention_logits, int geometry_dtype, void *output, float *grad_value,
+    float *grad_sampling_locations, float *grad_attention_logits, int64_t batch,
+    int64_t spatial_size, int64_t num_heads, int64_t channels, int64_t num_levels,
+    int64_t num_query, int64_t num_point, int64_t im2col_step, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  static const char *fn = "ms_deform_attn_forward_softmax_bin";
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               im2col_step};
+  msda::Shape s;
+  if (int rc = validate(fn, a, value_dtype, geometry_dtype, s)) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (needs_data(s) && s.lp > 0) {
+    if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
+        !attention_logits || !output || !grad_value || !grad_sampling_locations ||
+        !grad_attention_logits) {
+      return fail(MUSPACE_EINVAL, "%s: null tensor pointer", fn);
+    }
+    // the probabilities head the workspace, as in the softmax backward
+    const size_t pb = probs_bytes(s, geometry_dtype);
+    if (!workspace || workspace_bytes < pb || !aligned(workspace, 256)) {
+      return fail(MUSPACE_EINVAL,
+                  "%s: workspace of %zu bytes (256-byte aligned) required, got %zu", fn, pb,
+                  workspace_bytes);
+    }
+    unsigned char *tiles = static_cast<unsigned char *>(workspace) + pb;
+    bool fused = false;
+    with_dtypes(value_dtype, geometry_dtype, [&](auto vt, auto gt) {
+      fused = launch_forward_bin<decltype(vt), decltype(gt)>(
+          value, spatial_shapes, level_start_index, sampling_locations, attention_logits, output,
+          grad_value, grad_sampling_locations, grad_attention_logits, s, tiles,
+          workspace_bytes - pb, st, workspace);
+    });
+    if (fused) return check_launch(fn);
+  }
+  // the two calls this one stands for
+  if (int rc = ms_deform_attn_forward_softmax(value, value_dtype, spatial_shapes,
+                                              level_start_index, sampling_locations,
+                                              attention_logits, geometry_dtype, output, batch,
+                                              spatial_size, num_heads, channels, num_levels,
+                                              num_query, num_point, im2col_step, stream)) {
+    return rc;
+  }
+  return ms_deform_attn_backward_softmax_bin(
+      value, value_dtype, spatial_shapes, level_start_index, sampling_locations,
+      attention_logits, geometry_dtype, nullptr, grad_value, grad_sampling_locations,
+      grad_attention_logits, batch, spatial_size, num_heads, channels, num_levels, num_query,
+      num_point, im2col_step, workspace, workspace_bytes, stream);
+}
+
+int ms_deform_attn_forward_softmax_bin_fused(int value_dtype, int64_t batch,
+                                             int64_t spatial_size, int64_t num_heads,
+                                             int64_t channels, int64_t num_levels,
+                                             int64_t num_query, int64_t num_point) {
+  const Args a{batch, spatial_size, num_heads, channels, num_levels, num_query, num_point,
+               batch > 0 ? batch : 1};
+  msda::Shape s;
+  if (validate("ms_deform_attn_forward_softmax_bin_fused", a, value_dtype, value_dtype, s)) {
+    return 0;
+  }
+  ok();
+  TileWorkspace w;
+  int units = 0, slots = 0;
+  return needs_data(s) && s.lp > 0 && plan_tile_workspace(s, value_dtype, w) &&
+                 fwd_bin_fuses(s, value_dtype, w, units, slots, true)
+             ? 1
+             : 0;
 }
 
 int ms_deform_attn_backward_softmax_rest(

@@ -59,11 +59,18 @@ struct FwdBinArgs {
   float *grad_loc, *grad_attn, *grad_value;
   BinPlan p;                   // chunk_q = the forward block's units
   int slots;                   // tap slots per block: 4 wavefronts x steps x taps per step
+  void *probs;                 // PT != void: each sample's softmax probability, [.., L*P]
 };
 
-template <int C, int T>
+// PT: void, or the type in which the softmax probabilities are stored (the
+// forward with logits, msda_forward_softmax_bin_rows): sample() then takes
+// the sample's probability, stores it at the sample's place in `probs` (the
+// softmax backward reads it) and records it rounded to PT, the weight the
+// backward's tile kernel uses -- what binning the stored probabilities gives.
+template <int C, int T, typename PT = void>
 struct TileBinner {
   static constexpr bool kActive = true;
+  static constexpr bool kProbs = !std::is_void<PT>::value;
   FwdBinArgs a;
   int bm, ch, b, m, nt;
   const Level *lv;
@@ -111,8 +118,13 @@ struct TileBinner {
   __device__ __forceinline__ void sample(const Tap &t, int l, int q, int smp, float attn, bool ok,
                                          int slot, const Shape &s) {
     if (!ok) return;
+    const size_t o = (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp;
+    if constexpr (kProbs) {
+      const PT pr = from_float<PT>(attn);
+      static_cast<PT *>(a.probs)[o] = pr;
+      attn = to_float(pr);
+    }
     if (!t.in) {  // no corner inside the level: zero gradients, no record
-      const size_t o = (static_cast<size_t>(b * s.queries + q) * s.heads + m) * s.lp + smp;
       a.grad_attn[o] = 0.0f;
       *reinterpret_cast<float2 *>(a.grad_loc + 2 * o) = make_float2(0.0f, 0.0f);
       return;
@@ -210,6 +222,27 @@ __global__ void __launch_bounds__(kBlock)
   TileBinner<C, T> bin(args, fwd_bin_dyn, ntc, base, part, lb, s);
   forward_rows<VT, GT, C, NS, DenseRows<VT>, false, TileBinner<C, T>>(
       value, value_bytes, shapes, starts, loc, attn, DenseRows<VT>{out}, s, plan, lb, bin);
+}
+
+// The same with the attention weights given as logits (the softmax over each
+// unit's L*P samples fused into the prologue, forward_rows kSoftmax): every
+// sample's probability goes to args.probs (GT) and into its record. Only for
+// plans whose units are one step each (the host checks), where a sample's
+// probability is final when its tap is computed.
+template <typename VT, typename GT, int C, int NS, int T>
+__global__ void __launch_bounds__(kBlock)
+    msda_forward_softmax_bin_rows(const VT *__restrict__ value, uint32_t value_bytes,
+                                  const int64_t *__restrict__ shapes,
+                                  const int64_t *__restrict__ starts, const GT *__restrict__ loc,
+                                  const GT *__restrict__ logits, VT *__restrict__ out, Shape s,
+                                  RowPlan plan, FwdBinArgs args) {
+  extern __shared__ __align__(16) unsigned char fwd_bin_dyn[];
+  __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
+  __shared__ uint32_t part[kBlock / kWave];
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  TileBinner<C, T, GT> bin(args, fwd_bin_dyn, ntc, base, part, lb, s);
+  forward_rows<VT, GT, C, NS, DenseRows<VT>, true, TileBinner<C, T, GT>>(
+      value, value_bytes, shapes, starts, loc, logits, DenseRows<VT>{out}, s, plan, lb, bin);
 }
 
 }  // namespace msda

@@ -404,13 +404,21 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
     const Tap t = make_tap(lx, ly, L, ok);
     // the binning hook sees every live sample once: slot = its place in the
     // block's tap order (st < steps whenever ok)
-    if constexpr (Bin::kActive) {
-      bin.sample(t, l, tu.q, sm, ok ? a : 0.0f, ok, (wave * steps + st) * (NG * NS) + lane, s);
+    [[maybe_unused]] const int bin_slot = (wave * steps + st) * (NG * NS) + lane;
+    if constexpr (Bin::kActive && !kSoftmax) {
+      bin.sample(t, l, tu.q, sm, ok ? a : 0.0f, ok, bin_slot, s);
     }
     float ai = ok ? a : 0.0f;
     if constexpr (kSoftmax) {
       softmax_step(st);
       ai = e_cur;  // 0 unless ok
+      if constexpr (Bin::kActive) {
+        // the sample's probability exp(x - max) / sum, final here because
+        // the host fuses the binning only where a unit is one step (chunks
+        // == 1: the max and sum cover all of the unit's logits); the same
+        // 1/sum scales the unit's output row in end_step
+        bin.sample(t, l, tu.q, sm, ai * __builtin_amdgcn_rcpf(s_run), ok, bin_slot, s);
+      }
     }
     const uint32_t row = static_cast<uint32_t>(MC * VB);
     const uint32_t c00 = unit_base + static_cast<uint32_t>(L.start + t.cell00) * row;

@@ -11,11 +11,16 @@ softmax over each query's L*P samples per head and then call the operator:
 /root/reference/model_examples/BEVFormer/scripts/smoke_openmmlab.py:31-32).
 ``multi_scale_deformable_attn_softmax`` takes the logits instead. On ROCm
 tensors the forward row kernels compute the softmax in their prologue, so the
-weights are never written to or read back from HBM, and the backward needs no
-saved weights: its binning recomputes them into its scratch and its last step
-turns the weight gradient into the logit gradient, p * (g - sum_j p_j g_j).
-Gradients, dtypes and the early binning on a side stream follow
-``multi_scale_deformable_attn``.
+weights are never read back from HBM. Its backward's last step turns the
+weight gradient into the logit gradient, p * (g - sum_j p_j g_j). In training
+(a graph is recorded and an input needs a gradient) the forward also bins for
+the backward, as ``multi_scale_deformable_attn`` does: one call
+(ms_deform_attn_forward_softmax_bin) in which, where each query's L*P logits
+fit one step of the forward row kernel, the forward kernel writes every
+sample's probability to the backward's scratch and stores its records weighted
+by it; the backward then runs its second part only. Without a graph the
+forward writes nothing but the output, and the backward (if any) recomputes
+the probabilities. Gradients and dtypes follow ``multi_scale_deformable_attn``.
 """
 
 from __future__ import annotations
@@ -37,7 +42,6 @@ from .multi_scale_deformable_attn import (
     _native_extension,
     _reserve_early_buffers,
     _native_geometry_dtype,
-    _side_stream,
     _validate_inputs,
     multi_scale_deformable_attn_pytorch,
 )
@@ -53,11 +57,10 @@ def attention_softmax(attention_logits: torch.Tensor) -> torch.Tensor:
     )
 
 
-def _start_binning(ext, value, spatial, starts, sampling, logits, im2col_step):
-    """Workspace, gradients and the backward's first part (probabilities and
-    binning) on a side stream, ordered after the work that produced the inputs.
-    None when the early-binning budget is spent (the backward then runs in one
-    call)."""
+def _binning_buffers(ext, value, sampling, logits):
+    """Workspace (probabilities first, then the binning scratch) and float32
+    gradients for a forward that bins for its backward; None when the
+    early-binning budget is spent (the backward then runs in one call)."""
     release = _reserve_early_buffers(ext.backward_softmax_workspace_bytes(value, sampling),
                                      value, sampling, logits)
     if release is None:
@@ -76,18 +79,7 @@ def _start_binning(ext, value, spatial, starts, sampling, logits, im2col_step):
         torch.empty(sampling.shape, dtype=torch.float32, device=device),
         torch.empty(logits.shape, dtype=torch.float32, device=device),
     )
-    main = torch.cuda.current_stream(device)
-    side = _side_stream(device)
-    ready = torch.cuda.Event()
-    ready.record(main)
-    side.wait_event(ready)
-    ext.ms_deform_attn_backward_softmax_bin(value, spatial, starts, sampling, logits, *grads,
-                                            im2col_step, workspace, stream=side)
-    for tensor in (workspace, *grads, value, spatial, starts, sampling, logits):
-        tensor.record_stream(side)
-    done = torch.cuda.Event()
-    done.record(side)
-    return workspace, grads, done
+    return workspace, grads
 
 
 class _NativeMSDASoftmaxFunction(torch.autograd.Function):
@@ -115,10 +107,18 @@ class _NativeMSDASoftmaxFunction(torch.autograd.Function):
         ext.check_forward(value_arg, spatial_arg, start_arg, sampling_arg, logits_arg, output)
         ctx.binned = None
         if early_binning and any(ctx.needs_input_grad[i] for i in (0, 3, 4)):
-            ctx.binned = _start_binning(ext, value_arg, spatial_arg, start_arg, sampling_arg,
-                                        logits_arg, im2col_step)
-        ext.ms_deform_attn_forward_softmax(value_arg, spatial_arg, start_arg, sampling_arg,
-                                           logits_arg, output, im2col_step)
+            ctx.binned = _binning_buffers(ext, value_arg, sampling_arg, logits_arg)
+        if ctx.binned is not None:
+            # the forward and the backward's first part in one call: where the
+            # shape allows, the softmax-fused forward kernel itself writes the
+            # probabilities and stores the backward's records
+            workspace, grads = ctx.binned
+            ext.ms_deform_attn_forward_softmax_bin(value_arg, spatial_arg, start_arg,
+                                                   sampling_arg, logits_arg, output, *grads,
+                                                   im2col_step, workspace)
+        else:
+            ext.ms_deform_attn_forward_softmax(value_arg, spatial_arg, start_arg, sampling_arg,
+                                               logits_arg, output, im2col_step)
         ctx.save_for_backward(value_arg, spatial_arg, start_arg, sampling_arg, logits_arg)
         return output
 
@@ -131,8 +131,7 @@ class _NativeMSDASoftmaxFunction(torch.autograd.Function):
         grad = grad_output.to(value.dtype).contiguous()
         binned, ctx.binned = ctx.binned, None  # one backward per binning
         if binned is not None:
-            workspace, (grad_value, grad_sampling, grad_logits), done = binned
-            torch.cuda.current_stream(value.device).wait_event(done)
+            workspace, (grad_value, grad_sampling, grad_logits) = binned
             ext.ms_deform_attn_backward_softmax_rest(
                 value, spatial_shapes, level_start_index, sampling_locations, logits, grad,
                 grad_value, grad_sampling, grad_logits, ctx.im2col_step, workspace,

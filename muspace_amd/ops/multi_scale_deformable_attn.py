@@ -143,10 +143,9 @@ def _native_geometry_dtype(value: torch.Tensor, *geometry: torch.Tensor) -> torc
 # budget bounds what all forwards awaiting their backward may hold
 # (MUSPACE_EARLY_BINNING_BUDGET bytes, default 1/32 of the device's memory):
 # a forward that would exceed it does not bin early. The softmax operator
-# (msda_softmax.py) still bins on a second stream.
+# (msda_softmax.py) does the same through ms_deform_attn_forward_softmax_bin.
 EARLY_BINNING_ENV = "MUSPACE_EARLY_BINNING"
 EARLY_BINNING_BUDGET_ENV = "MUSPACE_EARLY_BINNING_BUDGET"
-_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
 
 
 class BinningBudget:
@@ -218,15 +217,6 @@ def _bins_early(*tensors: torch.Tensor) -> bool:
     input needs a gradient."""
     return (_early_binning_enabled() and torch.is_grad_enabled()
             and any(t.requires_grad for t in tensors))
-
-
-def _side_stream(device: torch.device) -> torch.cuda.Stream:
-    index = _device_index(device)
-    stream = _SIDE_STREAMS.get(index)
-    if stream is None:
-        stream = torch.cuda.Stream(device=index)  # default priority
-        _SIDE_STREAMS[index] = stream
-    return stream
 
 
 def _binning_buffers(ext, value, sampling, attn):

@@ -25,7 +25,7 @@ from pathlib import Path
 from typing import Any, Callable
 
 LIBRARY_RELPATH = "native/libmuspace_msda.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
@@ -103,6 +103,13 @@ _EXPORTS: dict[str, tuple[Any, list[Any]]] = {
         + [_c_int64] * 8
         + [_c_ptr, ctypes.c_size_t, _c_ptr],
     ),
+    "ms_deform_attn_forward_softmax_bin": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
+        + [_c_int64] * 8
+        + [_c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "ms_deform_attn_forward_softmax_bin_fused": (_c_int, [_c_int] + [_c_int64] * 7),
     "ms_deform_attn_backward_softmax": (
         _c_int,
         [_c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_ptr]
@@ -218,6 +225,8 @@ class NativeLibrary:
             "backward_softmax_workspace": self.backward_softmax_workspace,
             "ms_deform_attn_backward_softmax_bin": self.ms_deform_attn_backward_softmax_bin,
             "ms_deform_attn_backward_softmax_rest": self.ms_deform_attn_backward_softmax_rest,
+            "ms_deform_attn_forward_softmax_bin": self.ms_deform_attn_forward_softmax_bin,
+            "forward_softmax_bin_fuses": self.forward_softmax_bin_fuses,
             "ms_deform_attn_forward_scatter_div": self.ms_deform_attn_forward_scatter_div,
             "ms_deform_attn_forward_scatter_div_cams": self.ms_deform_attn_forward_scatter_div_cams,
             "deformable_aggregation_forward_opt": self.deformable_aggregation_forward_opt,
@@ -459,6 +468,16 @@ class NativeLibrary:
         return bool(self._raw["ms_deform_attn_forward_bin_fused"](
             _dtype_code(value.dtype), batch, spatial, heads, channels, levels, queries, points))
 
+    def forward_softmax_bin_fuses(self, value, sampling_locations) -> bool:
+        """Whether :meth:`ms_deform_attn_forward_softmax_bin` writes the
+        probabilities and stores the backward's records from the softmax-fused
+        forward kernel for these shapes (else it runs the softmax forward and
+        the softmax binning; same results)."""
+        batch, spatial, heads, channels = value.shape
+        _, queries, _, levels, points, _ = sampling_locations.shape
+        return bool(self._raw["ms_deform_attn_forward_softmax_bin_fused"](
+            _dtype_code(value.dtype), batch, spatial, heads, channels, levels, queries, points))
+
     def backward_workspace(self, value, sampling_locations):
         """Scratch of the tile-owned backward for these shapes (1 byte when the
         shape takes the atomic fallback)."""
@@ -565,17 +584,44 @@ class NativeLibrary:
         is checked before the first launch;
         :meth:`ms_deform_attn_backward_rest` on the same workspace and
         gradients must follow it on a stream ordered after this one."""
+        self._forward_bin_call("ms_deform_attn_forward_bin", False, value, spatial_shapes,
+                               level_start_index, sampling_locations, attention_weights, output,
+                               grad_value, grad_sampling_locations, grad_attention_weights,
+                               im2col_step, workspace)
+
+    def ms_deform_attn_forward_softmax_bin(
+        self, value, spatial_shapes, level_start_index, sampling_locations, attention_logits,
+        output, grad_value, grad_sampling_locations, grad_attention_logits, im2col_step,
+        workspace,
+    ) -> None:
+        """:meth:`ms_deform_attn_forward_softmax` and the first part of its
+        backward (:meth:`ms_deform_attn_backward_softmax_bin`) in one call on the
+        current stream, on a workspace of :meth:`backward_softmax_workspace`'s
+        size; :meth:`ms_deform_attn_backward_softmax_rest` on the same workspace
+        and gradients follows it. Where it applies the softmax-fused forward
+        kernel writes the probabilities and stores the backward's records itself."""
+        self._forward_bin_call("ms_deform_attn_forward_softmax_bin", True, value, spatial_shapes,
+                               level_start_index, sampling_locations, attention_logits, output,
+                               grad_value, grad_sampling_locations, grad_attention_logits,
+                               im2col_step, workspace)
+
+    def _forward_bin_call(
+        self, name, softmax, value, spatial_shapes, level_start_index, sampling_locations,
+        attention_weights, output, grad_value, grad_sampling_locations, grad_attention_weights,
+        im2col_step, workspace,
+    ) -> None:
+        """One of the forward + binning calls, every tensor and the workspace
+        size checked before the launch."""
         import torch
 
         self.check_forward(value, spatial_shapes, level_start_index, sampling_locations,
                            attention_weights, output)
         self._check_split(value, spatial_shapes, level_start_index, sampling_locations,
                           attention_weights, None, grad_value, grad_sampling_locations,
-                          grad_attention_weights, workspace, False)
+                          grad_attention_weights, workspace, softmax)
         batch, spatial, heads, channels = value.shape
         levels = spatial_shapes.shape[0]
         queries, points = sampling_locations.shape[1], sampling_locations.shape[4]
-        name = "ms_deform_attn_forward_bin"
         with torch.cuda.device(value.device):
             rc = self._raw[name](
                 value.data_ptr(), _dtype_code(value.dtype), spatial_shapes.data_ptr(),

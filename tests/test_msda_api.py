@@ -285,5 +285,5 @@ def test_early_binning_reservation_returns_when_the_workspace_allocation_fails(
         if which == "msda":
             msda_module._binning_buffers(FailingExtension(), value, sampling, attn)
         else:
-            softmax_module._start_binning(FailingExtension(), value, None, None, sampling, attn, 64)
+            softmax_module._binning_buffers(FailingExtension(), value, sampling, attn)
     assert budget.held(0) == 0

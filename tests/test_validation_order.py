@@ -92,18 +92,13 @@ def recording(monkeypatch, native_lib):
                 "hip", value.device.type, "simulated ROCm tensor selects native HIP backend"),
         )
 
-    def bins(ext_, *args):  # the side-stream part of _start_binning needs a GPU
-        ext_.calls.append("backward_workspace")
-        ext_.calls.append("ms_deform_attn_backward_bin")
-        return None
-
     def buffers(ext_, value, loc, attn):  # host stand-ins for the device buffers
         ext_.calls.append("backward_workspace")
         return (torch.empty(1 << 12, dtype=torch.uint8),
                 (torch.empty(value.shape), torch.empty(loc.shape), torch.empty(attn.shape)))
 
     monkeypatch.setattr(msda_module, "_binning_buffers", buffers)
-    monkeypatch.setattr(softmax_module, "_start_binning", bins)
+    monkeypatch.setattr(softmax_module, "_binning_buffers", buffers)
     monkeypatch.setenv("MUSPACE_EARLY_BINNING", "1")
     return ext
 
@@ -115,6 +110,15 @@ def test_valid_inputs_are_checked_then_binned_then_run(recording):
     assert recording.calls == ["check_forward", "backward_workspace",
                                "ms_deform_attn_forward_bin"]
     assert get_last_dispatch_report().selected_backend == "hip"
+
+
+def test_softmax_operator_is_checked_then_binned_then_run(recording):
+    """The softmax operator in training: one forward call that also bins."""
+    clear_dispatch_report()
+    out = softmax_module.multi_scale_deformable_attn_softmax(*_inputs(), backend="auto")
+    assert out.shape == (BATCH, QUERIES, HEADS * CHANNELS)
+    assert recording.calls == ["check_forward", "backward_workspace",
+                               "ms_deform_attn_forward_softmax_bin"]
 
 
 def _bad_host_spatial_shapes(t):
@@ -214,8 +218,11 @@ def test_binning_entry_checks_its_own_arguments(native_lib, raw_launches, part, 
     assert raw_launches == []
 
 
+@pytest.mark.parametrize("entry", ["ms_deform_attn_forward_bin",
+                                   "ms_deform_attn_forward_softmax_bin"])
 @pytest.mark.parametrize("case", sorted(BAD))
-def test_fused_forward_binning_entry_checks_its_own_arguments(native_lib, raw_launches, case):
+def test_fused_forward_binning_entry_checks_its_own_arguments(native_lib, raw_launches, entry,
+                                                               case):
     spoil, message = BAD[case]
     tensors = [t.detach() if t.dtype.is_floating_point else t for t in _inputs(False)]
     spoil(tensors)
@@ -223,8 +230,8 @@ def test_fused_forward_binning_entry_checks_its_own_arguments(native_lib, raw_la
     out = torch.empty(BATCH, QUERIES, HEADS * CHANNELS)
     workspace = torch.empty(1 << 20, dtype=torch.uint8)
     with pytest.raises(RuntimeError, match=message):
-        native_lib.ms_deform_attn_forward_bin(value, shapes, starts, loc, attn, out,
-                                              *_grads(value, loc, attn), 64, workspace)
+        getattr(native_lib, entry)(value, shapes, starts, loc, attn, out,
+                                   *_grads(value, loc, attn), 64, workspace)
     assert raw_launches == []
 
 
