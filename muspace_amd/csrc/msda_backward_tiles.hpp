@@ -195,6 +195,30 @@ __device__ __forceinline__ void zero_tile_cells(float *grad_value, size_t slab, 
   }
 }
 
+// Zero the C floats of each boundary cell of tile g (boundary_cell: its
+// first row when the tile is not at the level's top, its first column when
+// not at the left) inside the level, with `nthreads` threads. The cells are
+// enumerated (row 0, then column 0 below it) rather than filtered out of all
+// T * T (c4 bf16 step 2754 -> 2742 us).
+template <int C, int T>
+__device__ __forceinline__ void zero_boundary_cells(float *grad_value, size_t slab, int MC,
+                                                    const Level &L, const TileGeom &g, int tid,
+                                                    int nthreads) {
+  constexpr int C4 = C / 4;
+  const int top = g.y_lo > 0 ? 1 : 0, left = g.x_lo > 0 ? 1 : 0;
+  const int n_row = top * T, n_col = left * (T - top);
+  for (int i = tid; i < (n_row + n_col) * C4; i += nthreads) {
+    const int k = i / C4, c4 = (i % C4) * 4;
+    const int r = k < n_row ? 0 : top + (k - n_row);
+    const int c = k < n_row ? k : 0;
+    const int y = g.y_lo + r, x = g.x_lo + c;
+    if (y >= L.h || x >= L.w) continue;
+    *reinterpret_cast<float4 *>(grad_value + slab +
+                                static_cast<size_t>(L.start + y * L.w + x) * MC + c4) =
+        make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+}
+
 // Block-wide exclusive scan of per-thread run totals (kBinBlock threads);
 // returns this thread's offset, writes the grand total to *total. Only LDS
 // is exchanged, so the barriers leave global memory operations in flight.
@@ -316,8 +340,7 @@ __global__ void __launch_bounds__(kBinBlock)
   const size_t slab = static_cast<size_t>(b) * s.spatial * MC + m * C;
   for (int tl = grp; tl < nt; tl += groups) {
     const TileGeom g = tile_geom(tl, T, ntc, base);
-    zero_tile_cells<C, T>(grad_value, slab, MC, lv[g.l], g, threadIdx.x, blockDim.x,
-                          [&](int r, int c) { return boundary_cell(r, c, g); });
+    zero_boundary_cells<C, T>(grad_value, slab, MC, lv[g.l], g, threadIdx.x, blockDim.x);
   }
   __syncthreads();
   for (int j = 0; j < nsub; ++j) {
