@@ -113,16 +113,23 @@ def test_16bit_c16_two_steps_per_unit(vdt):
                 _oracle(value, shapes, loc, logits, grad, vdt, torch.float32), 2e-2, 2e-2)
 
 
-def test_minus_infinity_logits():
+@pytest.mark.parametrize("early", [False, True], ids=["one-call", "forward-binning"])
+def test_minus_infinity_logits(early):
     """Masked samples get weight zero; a unit whose logits are all -inf gives
-    NaN, as torch.softmax does (its output row and its logit gradients)."""
+    NaN, as torch.softmax does (its output row and its logit gradients);
+    through the plain entries and through the forward that bins (whose records
+    carry the probabilities)."""
     case = list(_case(9))
     logits = case[4]
     logits[0, 3, 1, 0, :] = float("-inf")       # one level masked
     logits[1, 5, 2, :, ::2] = float("-inf")     # every other point masked
     logits[1, 6, 0] = float("-inf")             # the whole unit
     value, shapes, starts, loc, logits, grad = case
-    out, gv, gl, glg = _native(*case)
+    if early:
+        (out, gv, gl, glg), fused = _native_early(*case)
+        assert fused
+    else:
+        out, gv, gl, glg = _native(*case)
     e_out, e_gv, e_gl, e_glg = _oracle(value, shapes, loc, logits, grad)
     torch.testing.assert_close(out, e_out, rtol=1e-5, atol=1e-5, equal_nan=True)
     assert torch.isnan(out[1, 6, 0:32]).all() and torch.isfinite(out[1, 6, 32:]).all()
