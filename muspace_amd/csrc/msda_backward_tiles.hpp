@@ -982,9 +982,14 @@ __global__ void __launch_bounds__(kTileBlock)
     }
   };
   auto store_value_tile = [&]() {
+    // the thread index through an empty asm: the slot addresses are
+    // recomputed here (a few instructions) rather than hoisted out of the
+    // batch loop, where they were held in registers through phase D
+    int me = tid;
+    asm volatile("" : "+v"(me));
 #pragma unroll
     for (int v = 0; v < VPT; ++v) {
-      const int unit = tid + v * kTileBlock;
+      const int unit = me + v * kTileBlock;
       // unit kk of cell c -> 16-byte slot c * (UPV + 1) + kk (the padding)
       if (unit < NPOS * UPV) reinterpret_cast<uint4 *>(vt)[unit + unit / UPV] = vt_next[v];
     }
@@ -1008,23 +1013,34 @@ __global__ void __launch_bounds__(kTileBlock)
       return grad_value + slab +
              static_cast<size_t>(Lw.start + (g.y_lo + r) * Lw.w + g.x_lo + c) * MC;
     };
+    // Position (r - dy, c - dx) of plane q = 2 dy + dx lies a fixed distance
+    // from position (r, c) of plane 0 (kQ1, kQ2, kQ3 floats for q = 1, 2, 3),
+    // so the four reads of a cell come off one address. They are issued before any is waited for:
+    // the empty asm takes all their values at once (scheduled freely, the
+    // compiler waited for each read before issuing the next, four LDS round
+    // trips per cell). Every cell (r, c) of [0, T]^2 gives addresses inside
+    // the four planes; a slot that is not the cell's is read and not added.
+    constexpr int kQ1 = NPOS * C - C, kQ2 = 2 * NPOS * C - TV * C;
+    constexpr int kQ3 = 3 * NPOS * C - (TV + 1) * C;
+    auto plane_base = [&](int r, int c, int ch) {
+      return planes + ((r + 1) * TV + c + 1) * C + ch;
+    };
     if (!split) {
       for (int i = tid; i < T * T * C4; i += kTileBlock) {
         const int cell = i / C4, ch = (i % C4) * 4;
         const int r = cell / T, c = cell % T;
-        if (g.y_lo + r >= Lw.h || g.x_lo + c >= Lw.w || boundary_cell(r, c, g)) continue;
-        float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float *pl = plane_base(r, c, ch);
+        float4 v[4];
+        v[0] = *reinterpret_cast<const float4 *>(pl);
+        v[1] = *reinterpret_cast<const float4 *>(pl + kQ1);
+        v[2] = *reinterpret_cast<const float4 *>(pl + kQ2);
+        v[3] = *reinterpret_cast<const float4 *>(pl + kQ3);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int pr = r - (q >> 1), pc = c - (q & 1);  // position, >= -1
-          const float4 v = *reinterpret_cast<const float4 *>(
-              planes + (q * NPOS + (pr + 1) * TV + pc + 1) * C + ch);
-          sum.x += v.x;
-          sum.y += v.y;
-          sum.z += v.z;
-          sum.w += v.w;
-        }
-        const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
+        for (int q = 0; q < 4; ++q)
+          asm volatile("" : "+v"(v[q].x), "+v"(v[q].y), "+v"(v[q].z), "+v"(v[q].w));
+        if (g.y_lo + r >= Lw.h || g.x_lo + c >= Lw.w || boundary_cell(r, c, g)) continue;
+        const float sv[4] = {v[0].x + v[1].x + v[2].x + v[3].x, v[0].y + v[1].y + v[2].y + v[3].y,
+                             v[0].z + v[1].z + v[2].z + v[3].z, v[0].w + v[1].w + v[2].w + v[3].w};
         store16_nt(cell_ptr(r, c) + ch, sv);
       }
     }
@@ -1052,13 +1068,14 @@ __global__ void __launch_bounds__(kTileBlock)
         r = top + (k - TV - T - top * T);
         c = 0;
       }
+      const float *pl = plane_base(r, c, ch);
+      float v0 = pl[0], v1 = pl[kQ1], v2 = pl[kQ2], v3 = pl[kQ3];
+      asm volatile("" : "+v"(v0), "+v"(v1), "+v"(v2), "+v"(v3));
       if (g.y_lo + r >= Lw.h || g.x_lo + c >= Lw.w) continue;
-      float sum = 0.0f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int pr = r - (q >> 1), pc = c - (q & 1);  // position, >= -1
-        if (pr < T && pc < T) sum += planes[(q * NPOS + (pr + 1) * TV + pc + 1) * C + ch];
-      }
+      // plane q holds a position of the tile (row and column < T) for
+      // q = 0 when r, c < T, q = 1 when r < T, q = 2 when c < T, q = 3 always
+      const float sum =
+          (r < T && c < T ? v0 : 0.0f) + (r < T ? v1 : 0.0f) + (c < T ? v2 : 0.0f) + v3;
       unsafeAtomicAdd(cell_ptr(r, c) + ch, sum);
     }
   };
@@ -1374,23 +1391,39 @@ __global__ void __launch_bounds__(kTileBlock)
         }
       }
       if (sub == S - 1) {
+        float *pb = planes + p_id * C + k * CPL;  // slot p_id of plane d at pb + d * NPOS * C
+        if (!first_of_item) {
+          // the item's earlier batches' sums: all reads issued before any is
+          // waited for (the empty asm takes them together; scheduled freely,
+          // each read was waited for before the next was issued)
+          float4 old[4][CPL / 4];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          float4 *dst = reinterpret_cast<float4 *>(planes + (d * NPOS + p_id) * C + k * CPL);
+          for (int d = 0; d < 4; ++d)
 #pragma unroll
-          for (int h = 0; h < CPL / 4; ++h) {
-            float4 cur = make_float4(acc[4 * h][d], acc[4 * h + 1][d], acc[4 * h + 2][d],
-                                     acc[4 * h + 3][d]);
-            if (!first_of_item) {
-              const float4 old = dst[h];
-              cur.x += old.x;
-              cur.y += old.y;
-              cur.z += old.z;
-              cur.w += old.w;
+            for (int h = 0; h < CPL / 4; ++h)
+              old[d][h] = reinterpret_cast<const float4 *>(pb + d * NPOS * C)[h];
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int h = 0; h < CPL / 4; ++h)
+              asm volatile("" : "+v"(old[d][h].x), "+v"(old[d][h].y), "+v"(old[d][h].z),
+                           "+v"(old[d][h].w));
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int h = 0; h < CPL / 4; ++h) {
+              acc[4 * h][d] += old[d][h].x;
+              acc[4 * h + 1][d] += old[d][h].y;
+              acc[4 * h + 2][d] += old[d][h].z;
+              acc[4 * h + 3][d] += old[d][h].w;
             }
-            dst[h] = cur;
-          }
         }
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+          for (int h = 0; h < CPL / 4; ++h)
+            reinterpret_cast<float4 *>(pb + d * NPOS * C)[h] = make_float4(
+                acc[4 * h][d], acc[4 * h + 1][d], acc[4 * h + 2][d], acc[4 * h + 3][d]);
       }
     }
     lds_barrier();
