@@ -881,6 +881,7 @@ __global__ void __launch_bounds__(kTileBlock)
       static_cast<uint32_t>(static_cast<uint64_t>(n_items) * (xcd + 1) / kXcdQueues);
   uint32_t *queue = item_total + 1 + xcd;
   __shared__ uint32_t taken[2];
+  __shared__ Item taken_item;  // descriptor of taken[0], fetched by wavefront 0
   auto take_item = [&]() -> uint32_t {  // thread 0 only
     const uint32_t i = lo < hi ? atomicAdd(queue, 1u) : 0u;
     return lo + i < hi ? lo + i : kNoItem;
@@ -1468,11 +1469,28 @@ __global__ void __launch_bounds__(kTileBlock)
     if (tid < kWave) bucket[tid] = 0;
     if (last_of_item) write_back(c0.d);
     load_value_tile(c1.d, next_new_item);
-    if (refill && tid == 0) taken[0] = lo + took < hi ? lo + took : kNoItem;
+    if (refill && wave == 0) {
+      // wavefront 0 fetches the taken item's descriptor (scalar loads) and
+      // hands it over through LDS: it has slack before the barrier (the other
+      // wavefronts finish phase E later), where every workgroup loading it
+      // after the barrier waited a scalar memory round trip in the next
+      // batch's first phase
+      const uint32_t t = __builtin_amdgcn_readfirstlane(took);
+      const uint32_t idx = lo + t < hi ? lo + t : kNoItem;
+      bool ok;
+      const Item d = item_of(idx, ok);
+      if (lane == 0) {
+        taken[0] = idx;
+        taken_item = d;
+      }
+    }
     c0 = c1;
     c1 = advance(c1);
     lds_barrier();
-    if (refill) pre = item_of(taken[0], pre_ok);
+    if (refill) {
+      pre_ok = taken[0] != kNoItem;
+      pre = taken_item;
+    }
     if (!c0.valid) break;
   }
 }
