@@ -79,6 +79,10 @@ struct BinPlan {
   // record); 0: it stores them over the record and msda_grad_gather copies
   // them into sample order through rec_of_sample.
   int direct;
+  // 1: bin_count keeps its LDS histograms as two 16-bit counters per word
+  // (a chunk has fewer than 65536 samples), half the LDS, twice the blocks
+  // per CU where the histograms limit them
+  int hist16;
 };
 
 // One work item: records [r0, r1) of one tile of the (b, m) slab. `tile`
@@ -251,7 +255,9 @@ __global__ void __launch_bounds__(kBinBlock)
                    float *__restrict__ grad_value) {
   __shared__ Level lv[kMaxLevels];
   __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
-  extern __shared__ uint32_t hist[];  // [count_sub][nt]
+  // [count_sub][nt] counters: one per word, or (hist16) counter i in the
+  // 16-bit half i & 1 of word i >> 1
+  extern __shared__ uint32_t hist[];
   stage_levels(lv, shapes, starts, s);
   stage_tiles<T>(lv, s.levels, ntc, base);
   const int nt = base[s.levels];
@@ -259,7 +265,16 @@ __global__ void __launch_bounds__(kBinBlock)
   const int bm = blockIdx.x / groups, grp = blockIdx.x % groups;
   const int ch0 = grp * p.count_sub;
   const int nsub = min(p.count_sub, p.chunks - ch0);
-  for (int i = threadIdx.x; i < nsub * nt; i += blockDim.x) hist[i] = 0;
+  const bool h16 = p.hist16 != 0;
+  const int hwords = h16 ? (nsub * nt + 1) >> 1 : nsub * nt;
+  for (int i = threadIdx.x; i < hwords; i += blockDim.x) hist[i] = 0;
+  auto count_one = [&](int i) {
+    if (h16) {
+      atomicAdd(&hist[i >> 1], 1u << ((i & 1) << 4));
+    } else {
+      atomicAdd(&hist[i], 1u);
+    }
+  };
   // the item counter and the tile kernel's per-XCD take counters
   if (blockIdx.x == 0 && threadIdx.x <= kXcdQueues) item_total[threadIdx.x] = 0;
   __syncthreads();
@@ -305,7 +320,7 @@ __global__ void __launch_bounds__(kBinBlock)
         const int i = i0 + u * kBinBlock;
         const Tap t = make_tap(lx[u], ly[u], L, live[u]);
         const int row = (i >> p.lp_log2) >> cq_log2;  // chunk of the group
-        if (t.in) atomicAdd(&hist[row * nt + primary_tile<T>(t, tnc, tbase)], 1u);
+        if (t.in) count_one(row * nt + primary_tile<T>(t, tnc, tbase));
       }
     }
   } else {
@@ -330,7 +345,7 @@ __global__ void __launch_bounds__(kBinBlock)
         const int l = level_of_sample(live[u] ? smp[u] : 0, s);
         const Tap t = make_tap(lx[u], ly[u], lv[l], live[u]);
         const int row = (i >> p.lp_log2) >> cq_log2;  // chunk of the group
-        if (t.in) atomicAdd(&hist[row * nt + primary_tile<T>(t, ntc[l], base[l])], 1u);
+        if (t.in) count_one(row * nt + primary_tile<T>(t, ntc[l], base[l]));
       }
     }
   }
@@ -345,7 +360,10 @@ __global__ void __launch_bounds__(kBinBlock)
   __syncthreads();
   for (int j = 0; j < nsub; ++j) {
     uint32_t *row = counts + (static_cast<size_t>(bm) * p.chunks + ch0 + j) * p.tile_bound;
-    for (int i = threadIdx.x; i < nt; i += blockDim.x) row[i] = hist[j * nt + i];
+    for (int i = threadIdx.x; i < nt; i += blockDim.x) {
+      const int k = j * nt + i;
+      row[i] = h16 ? (hist[k >> 1] >> ((k & 1) << 4)) & 0xffffu : hist[k];
+    }
   }
 }
 

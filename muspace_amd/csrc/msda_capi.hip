@@ -638,6 +638,14 @@ bool fwd_bin_chunk(const msda::Shape &s, int value_dtype, int &units, int &slots
 // bin_count blocks per slab: groups of count_sub chunks.
 int count_groups(const msda::BinPlan &p) { return (p.chunks + p.count_sub - 1) / p.count_sub; }
 
+// bin_count's LDS histograms (count_sub rows of tile_bound counters), with
+// 16-bit counters where a chunk has fewer than 65536 samples.
+size_t count_hist_bytes(msda::BinPlan &p) {
+  p.hist16 = (static_cast<int64_t>(p.chunk_q) << p.lp_log2) < 65536 ? 1 : 0;
+  const size_t counters = static_cast<size_t>(p.tile_bound) * p.count_sub;
+  return p.hist16 ? (counters + 1) / 2 * 4 : counters * 4;
+}
+
 // Scratch layout of the tile-owned backward.
 struct TileWorkspace {
   msda::BinPlan plan;
@@ -656,6 +664,7 @@ bool plan_tile_workspace(const msda::Shape &s, int value_dtype, TileWorkspace &w
   p.chunk_q = per_q > msda::kBinBlock ? per_q : msda::kBinBlock;
   p.chunks = (s.queries + p.chunk_q - 1) / p.chunk_q;
   p.count_sub = 1;
+  p.hist16 = 0;  // set per launch (count_hist_bytes)
   // a level of n cells has ceil(h/T)*ceil(w/T) <= n/T + 1 tiles
   const int64_t bound = static_cast<int64_t>(s.spatial) / T + s.levels + 1;
   if (bound > msda::kMaxTilesPerSlab) return false;
@@ -748,13 +757,13 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   uint32_t *rec_of_sample = reinterpret_cast<uint32_t *>(ws + w.rec_of_sample);
   msda::Item *items = reinterpret_cast<msda::Item *>(ws + w.items);
   uint32_t *item_total = reinterpret_cast<uint32_t *>(ws + w.item_total);
-  const msda::BinPlan &p = w.plan;
+  msda::BinPlan p = w.plan;
   const int bm = s.batch * s.heads;
   const VT *v = static_cast<const VT *>(value);
   const GT *lc = static_cast<const GT *>(loc);
   const GT *aw = static_cast<const GT *>(attn);
   const VT *go = static_cast<const VT *>(grad_out);
-  const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4 * p.count_sub;
+  const size_t hist_bytes = count_hist_bytes(p);
 
   auto count = msda::msda_bin_count<GT, C, T>;
   auto scatter = msda::msda_bin_scatter<GT, C, T>;
@@ -851,7 +860,7 @@ bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const in
   p.count_sub = sub > 1 ? sub : 1;
   const GT *lc = static_cast<const GT *>(loc);
   const GT *aw = static_cast<const GT *>(attn);
-  const size_t hist_bytes = static_cast<size_t>(p.tile_bound) * 4 * p.count_sub;
+  const size_t hist_bytes = count_hist_bytes(p);
   auto count = msda::msda_bin_count<GT, C, T>;
   (void)hipFuncSetAttribute(reinterpret_cast<const void *>(count),
                             hipFuncAttributeMaxDynamicSharedMemorySize, hist_bytes);

@@ -117,7 +117,9 @@ def small_case(seed, batch, queries, heads, channels, levels, points, lo=-0.1, h
 
 # (batch, queries, heads, channels, levels, points): reference test shapes
 # (odd channels, generic kernels) and row-kernel shapes covering every
-# samples-per-query layout (L*P = 1, 2, 3, 4, 5, 8, 12, 16, 32, 40, 64).
+# samples-per-query layout (L*P = 1, 2, 3, 4, 5, 8, 12, 16, 32, 40, 64), and
+# L*P = 256, where a binning chunk (256 queries) holds 65536 samples, past
+# bin_count's 16-bit histogram counters.
 SMALL = [
     (1, 5, 2, 3, ((2, 2),), 4),
     (2, 3, 4, 2, ((1, 3), (2, 1)), 2),
@@ -137,6 +139,7 @@ SMALL = [
     (2, 21, 8, 16, ((9, 10), (4, 5)), 4),
     (2, 21, 4, 64, ((9, 10), (4, 5)), 4),
     (1, 15, 8, 12, ((9, 10), (4, 5)), 4),
+    (1, 300, 2, 32, ((10, 12), (5, 6), (3, 3), (2, 2)), 64),
 ]
 DTYPES = [
     (torch.float32, torch.float32),
