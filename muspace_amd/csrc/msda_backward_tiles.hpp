@@ -14,8 +14,12 @@
 //                  histogram in LDS. Also zeroes the gradients of samples
 //                  with no corner inside their level and the tile-boundary
 //                  cells of grad_value (see below).
-//   2. bin_scan    per (b, m): exclusive scan of the histograms -> per-chunk
-//                  write cursors and per-tile record ranges; one work item
+//   2. bin_cursors per (b, m) and group of tiles: each tile's histogram
+//                  entries -> per-chunk write cursors relative to the tile's
+//                  first record, and the tile's record count;
+//      bin_scan    per (b, m): exclusive scan of the tile counts -> per-tile
+//                  record ranges (writers add a tile's start to its chunk
+//                  cursor); one work item
 //                  per tile, or several of at most `rmax` records for a tile
 //                  holding more ("split"); items appended, coarsest level
 //                  first, to one compact list; zeroes the cells of empty and
@@ -367,13 +371,91 @@ __global__ void __launch_bounds__(kBinBlock)
   }
 }
 
+// ---------------------------------------------------------- 2. cursors ---
+
+constexpr int kCurBlock = 256;  // bin_cursors workgroup
+
+// Per tile of a slab, the per-chunk counts -> each chunk's write cursor
+// relative to the tile's first record (exclusive prefix over chunks, in
+// place), and the tile's record count to tile_start[slab][tile] (bin_scan
+// then turns the counts into the tiles' offsets; the records' writers add
+// the tile's offset to its chunk cursor). Grid: slabs x gridDim.y blocks; a
+// block takes groups of kCurBlock / S consecutive tiles (group blockIdx.y,
+// blockIdx.y + gridDim.y, ...), S threads a tile (S = 1 << seg_log2): thread
+// (seg, t) sums and rewrites chunks [seg * per, (seg + 1) * per) of tile t,
+// consecutive lanes on consecutive tiles, so each chunk's counts are read
+// as one run. One block a slab, a thread a tile, took 18-33 us at the
+// benchmark shapes: a slab's counts (chunks x tiles words, up to 160 k at c3)
+// went through one CU.
+template <int T>
+__global__ void __launch_bounds__(kCurBlock)
+    msda_bin_cursors(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
+                     Shape s, BinPlan p, int seg_log2, uint32_t *__restrict__ counts,
+                     uint32_t *__restrict__ tile_start) {
+  __shared__ Level lv[kMaxLevels];
+  __shared__ int ntc[kMaxLevels], base[kMaxLevels + 1];
+  __shared__ uint32_t segsum[kCurBlock];
+  stage_levels(lv, shapes, starts, s);
+  stage_tiles<T>(lv, s.levels, ntc, base);
+  const int nt = base[s.levels];
+  const int bm = blockIdx.x;
+  const int S = 1 << seg_log2, tpb = kCurBlock >> seg_log2;
+  const int tl = static_cast<int>(threadIdx.x) & (tpb - 1);
+  const int seg = static_cast<int>(threadIdx.x) >> (8 - seg_log2);  // kCurBlock = 256
+  const int per = (p.chunks + S - 1) >> seg_log2;
+  const int c0 = seg * per, c1 = min(p.chunks, c0 + per);
+  uint32_t *cnt = counts + static_cast<size_t>(bm) * p.chunks * p.tile_bound;
+  uint32_t *ts = tile_start + static_cast<size_t>(bm) * (p.tile_bound + 1);
+  constexpr int kRound = 16;  // counts in flight per thread
+  for (int g = blockIdx.y; g * tpb < nt; g += gridDim.y) {
+    const int t = g * tpb + tl;
+    const bool ok = t < nt;
+    const int tc = ok ? t : nt - 1;  // clamped: every load is issued
+    uint32_t sum = 0;
+    for (int cb = c0; cb < c1; cb += kRound) {
+      uint32_t v[kRound];
+#pragma unroll
+      for (int j = 0; j < kRound; ++j) {
+        v[j] = cnt[static_cast<size_t>(min(cb + j, p.chunks - 1)) * p.tile_bound + tc];
+      }
+#pragma unroll
+      for (int j = 0; j < kRound; ++j) sum += cb + j < c1 ? v[j] : 0u;
+    }
+    segsum[threadIdx.x] = sum;
+    lds_barrier();
+    uint32_t before = 0, total = 0;
+    for (int k = 0; k < S; ++k) {
+      const uint32_t v = segsum[k * tpb + tl];
+      before += k < seg ? v : 0u;
+      total += v;
+    }
+    if (ok && seg == 0) ts[t] = total;
+    uint32_t cur = before;
+    for (int cb = c0; cb < c1; cb += kRound) {
+      uint32_t v[kRound];
+#pragma unroll
+      for (int j = 0; j < kRound; ++j) {
+        v[j] = cnt[static_cast<size_t>(min(cb + j, p.chunks - 1)) * p.tile_bound + tc];
+      }
+#pragma unroll
+      for (int j = 0; j < kRound; ++j) {
+        if (ok && cb + j < c1) {
+          cnt[static_cast<size_t>(cb + j) * p.tile_bound + t] = cur;
+          cur += v[j];
+        }
+      }
+    }
+    lds_barrier();  // segsum is rewritten by the next group
+  }
+}
+
 // ------------------------------------------------------------- 2. scan ---
 
 template <int C, int T>
 __global__ void __launch_bounds__(kBinBlock)
     msda_bin_scan(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
-                  Shape s, BinPlan p, uint32_t *__restrict__ counts,
-                  uint32_t *__restrict__ tile_start, uint32_t *__restrict__ item_total,
+                  Shape s, BinPlan p, uint32_t *__restrict__ tile_start,
+                  uint32_t *__restrict__ item_total,
                   Item *__restrict__ items, uint32_t *__restrict__ zero_tiles,
                   float *__restrict__ grad_value) {
   __shared__ Level lv[kMaxLevels];
@@ -386,56 +468,21 @@ __global__ void __launch_bounds__(kBinBlock)
   const int nt = base[s.levels];
   const int bm = blockIdx.x;
   const int b = bm / s.heads, m = bm % s.heads;
-  uint32_t *cnt = counts + static_cast<size_t>(bm) * p.chunks * p.tile_bound;
   uint32_t *ts = tile_start + static_cast<size_t>(bm) * (p.tile_bound + 1);
   if (threadIdx.x == 0) zero_count = 0;
 
-  // each thread owns a contiguous run of tiles. The per-chunk counts are
-  // read kScanBlock at a time, all loads of a block before its stores (a
-  // load after a store to the same array could not be moved ahead of it, and
-  // the read-modify-write per chunk was one memory round trip each; 64 in
-  // flight measured no faster with the fused forward's 157 chunks per slab).
-  constexpr int kScanBlock = 16;
+  // each thread owns a contiguous run of tiles: their record counts
+  // (bin_cursors) -> their offsets in the slab's records
   const int per = (nt + kBinBlock - 1) / kBinBlock;
   const int t0 = min(nt, static_cast<int>(threadIdx.x) * per), t1 = min(nt, t0 + per);
   uint32_t run = 0;
-  for (int t = t0; t < t1; ++t) {
-    uint32_t tot = 0;
-    for (int c0 = 0; c0 < p.chunks; c0 += kScanBlock) {
-      uint32_t v[kScanBlock];
-#pragma unroll
-      for (int j = 0; j < kScanBlock; ++j) {
-        const int c = min(c0 + j, p.chunks - 1);
-        v[j] = cnt[static_cast<size_t>(c) * p.tile_bound + t];
-      }
-#pragma unroll
-      for (int j = 0; j < kScanBlock; ++j) tot += c0 + j < p.chunks ? v[j] : 0u;
-    }
-    ts[t] = tot;  // the tile's record count until it is replaced by its offset
-    run += tot;
-  }
+  for (int t = t0; t < t1; ++t) run += ts[t];
   uint32_t total;
   uint32_t off = block_exclusive(run, part, &total);
   if (threadIdx.x == 0) ts[nt] = total;
   for (int t = t0; t < t1; ++t) {
     const uint32_t n = ts[t];
     ts[t] = off;
-    uint32_t cur = off;
-    for (int c0 = 0; c0 < p.chunks; c0 += kScanBlock) {
-      uint32_t v[kScanBlock];
-#pragma unroll
-      for (int j = 0; j < kScanBlock; ++j) {
-        const int c = min(c0 + j, p.chunks - 1);
-        v[j] = cnt[static_cast<size_t>(c) * p.tile_bound + t];
-      }
-#pragma unroll
-      for (int j = 0; j < kScanBlock; ++j) {
-        if (c0 + j < p.chunks) {
-          cnt[static_cast<size_t>(c0 + j) * p.tile_bound + t] = cur;
-          cur += v[j];
-        }
-      }
-    }
     off += n;
   }
   __syncthreads();
@@ -540,7 +587,9 @@ template <typename GT, int C, int T>
 __global__ void __launch_bounds__(kBinBlock)
     msda_bin_scatter(const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                      const GT *__restrict__ loc, const GT *__restrict__ attn, Shape s, BinPlan p,
-                     const uint32_t *__restrict__ counts, const uint32_t *__restrict__ zero_tiles,
+                     const uint32_t *__restrict__ counts,
+                     const uint32_t *__restrict__ tile_start,
+                     const uint32_t *__restrict__ zero_tiles,
                      uint4 *__restrict__ records, uint32_t *__restrict__ rec_of_sample,
                      float *__restrict__ grad_loc, float *__restrict__ grad_attn,
                      float *__restrict__ grad_value) {
@@ -556,7 +605,8 @@ __global__ void __launch_bounds__(kBinBlock)
   stage_tiles<T>(lv, s.levels, ntc, base);
   const int nt = base[s.levels];
   const uint32_t *row = counts + static_cast<size_t>(blockIdx.x) * p.tile_bound;
-  for (int i = threadIdx.x; i < nt; i += blockDim.x) cursor[i] = row[i];
+  const uint32_t *ts_row = tile_start + static_cast<size_t>(blockIdx.x / p.chunks) * (p.tile_bound + 1);
+  for (int i = threadIdx.x; i < nt; i += blockDim.x) cursor[i] = ts_row[i] + row[i];
 
   const int bm = blockIdx.x / p.chunks, ch = blockIdx.x % p.chunks;
   const int b = bm / s.heads, m = bm % s.heads;

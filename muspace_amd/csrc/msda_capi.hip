@@ -646,6 +646,22 @@ size_t count_hist_bytes(msda::BinPlan &p) {
   return p.hist16 ? (counters + 1) / 2 * 4 : counters * 4;
 }
 
+// bin_cursors over the counts bin_count wrote: S = 1 << seg_log2 threads a
+// tile, so that a thread takes at most 32 chunks (S <= 16), and about 512
+// blocks in all (at most 32 a slab).
+template <int T>
+void launch_bin_cursors(const int64_t *shapes, const int64_t *starts, const msda::Shape &s,
+                        const msda::BinPlan &p, int bm, uint32_t *counts, uint32_t *tile_start,
+                        hipStream_t st) {
+  int seg_log2 = 0;
+  while (seg_log2 < 4 && ((p.chunks + (1 << seg_log2) - 1) >> seg_log2) > 32) ++seg_log2;
+  int gy = 512 / (bm > 0 ? bm : 1);
+  gy = gy < 1 ? 1 : (gy > 32 ? 32 : gy);
+  msda::msda_bin_cursors<T><<<dim3(bm, gy), msda::kCurBlock, 0, st>>>(shapes, starts, s, p,
+                                                                      seg_log2, counts,
+                                                                      tile_start);
+}
+
 // Scratch layout of the tile-owned backward.
 struct TileWorkspace {
   msda::BinPlan plan;
@@ -780,10 +796,12 @@ void launch_backward_tiles(const void *value, const int64_t *shapes, const int64
   if (phase != Phase::kRest) {
     count<<<bm * count_groups(p), msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p,
                                                                      counts, item_total, gv);
+    launch_bin_cursors<T>(shapes, starts, s, p, bm, counts, tile_start, st);
     msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
-        shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
+        shapes, starts, s, p, tile_start, item_total, items, zero_tiles, gv);
     scatter<<<bm * p.chunks, msda::kBinBlock, scatter_bytes, st>>>(
-        shapes, starts, lc, aw, s, p, counts, zero_tiles, records, rec_of_sample, gl, ga, gv);
+        shapes, starts, lc, aw, s, p, counts, tile_start, zero_tiles, records, rec_of_sample, gl,
+        ga, gv);
   }
   if (phase == Phase::kBin) return;
   const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
@@ -866,9 +884,11 @@ bool launch_forward_bin_tiles(const void *value, const int64_t *shapes, const in
                             hipFuncAttributeMaxDynamicSharedMemorySize, hist_bytes);
   count<<<bm * count_groups(p), msda::kBinBlock, hist_bytes, st>>>(shapes, starts, lc, s, p,
                                                                    counts, item_total, gv);
+  launch_bin_cursors<T>(shapes, starts, s, p, bm, counts, tile_start, st);
   msda::msda_bin_scan<C, T><<<bm, msda::kBinBlock, 0, st>>>(
-      shapes, starts, s, p, counts, tile_start, item_total, items, zero_tiles, gv);
-  const msda::FwdBinArgs args{counts, zero_tiles, records, gl, ga, gv, p, slots, probs};
+      shapes, starts, s, p, tile_start, item_total, items, zero_tiles, gv);
+  const msda::FwdBinArgs args{counts, tile_start, zero_tiles, records, gl, ga,
+                              gv,     p,          slots,      probs};
   const size_t lds = msda::fwd_bin_lds_bytes(slots, p.tile_bound);
   const uint32_t vbytes = static_cast<uint32_t>(value_bytes(s, sizeof(VT)));
   forward_rows_ns<VT, C>(s, [&](auto ns, const Launch &L) {

@@ -6,7 +6,7 @@
 // (bin_count -> bin_scan -> bin_scatter) reads the geometry twice and, on a
 // second stream beside the forward, gains nothing: the forward row kernel
 // holds 242 VGPRs per wavefront, so no binning wavefront fits next to it and
-// the binning runs after it. Here bin_count and bin_scan run first, with
+// the binning runs after it. Here bin_count, bin_cursors and bin_scan run first, with
 // query chunks that are exactly the forward's blocks, and the forward block
 // that computes a chunk's taps also writes the chunk's records:
 //
@@ -15,7 +15,7 @@
 //             place in the block's tap order; a sample with no corner in its
 //             level gets zero location/weight gradients (or no record);
 //   finish(): the block's tile counts scanned, the staged records sorted by
-//             tile in LDS and stored in tile order at bin_scan's cursors
+//             tile in LDS and stored in tile order at the binning's cursors
 //             (consecutive threads, consecutive records of one tile), then
 //             the cells of the slab's empty and split tiles zeroed
 //             (bin_scatter's duties).
@@ -53,7 +53,8 @@ __host__ __device__ constexpr size_t fwd_bin_lds_bytes(int slots, int tile_bound
 
 // Host-built arguments of the fused binning.
 struct FwdBinArgs {
-  const uint32_t *cursors;     // bin_scan's per-(chunk, tile) record cursors
+  const uint32_t *cursors;     // bin_cursors' per-(chunk, tile) cursors, relative to the tile
+  const uint32_t *tile_start;  // bin_scan's per-slab tile offsets
   const uint32_t *zero_tiles;  // per slab {count, tile...}: empty and split tiles
   uint4 *records;
   float *grad_loc, *grad_attn, *grad_value;
@@ -167,10 +168,12 @@ struct TileBinner {
     }
     lds_barrier();
     // records out in tile order: consecutive i of one tile are consecutive
-    // records of the range bin_scan gave this chunk in that tile. The
-    // cursors (L2-resident) are loaded for all of a thread's records first.
+    // records of this chunk's range in that tile (the tile's start plus the
+    // chunk's cursor). The cursors and starts (L2-resident) are loaded for
+    // all of a thread's records first.
     constexpr int U = kFwdBinSlots / kBlock;
     const uint32_t *cur_row = a.cursors + static_cast<size_t>(lb_row()) * a.p.tile_bound;
+    const uint32_t *ts_row = a.tile_start + static_cast<size_t>(bm) * (a.p.tile_bound + 1);
     uint4 *rec = a.records + static_cast<size_t>(bm) * a.p.rec_cap;
     uint32_t slot[U], at[U], cur[U];
 #pragma unroll
@@ -179,7 +182,7 @@ struct TileBinner {
       slot[u] = i < static_cast<int>(total) ? sorted[i] : 0u;
       const uint32_t tile = i < static_cast<int>(total) ? keys[slot[u]] >> 16 : 0u;
       at[u] = static_cast<uint32_t>(i) - loff[tile];
-      cur[u] = cur_row[tile];
+      cur[u] = ts_row[tile] + cur_row[tile];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
