@@ -373,7 +373,8 @@ __global__ void __launch_bounds__(kBinBlock)
 
 // ---------------------------------------------------------- 2. cursors ---
 
-constexpr int kCurBlock = 256;  // bin_cursors workgroup
+constexpr int kCurBlockLog2 = 8;
+constexpr int kCurBlock = 1 << kCurBlockLog2;  // bin_cursors workgroup
 
 // Per tile of a slab, the per-chunk counts -> each chunk's write cursor
 // relative to the tile's first record (exclusive prefix over chunks, in
@@ -401,7 +402,7 @@ __global__ void __launch_bounds__(kCurBlock)
   const int bm = blockIdx.x;
   const int S = 1 << seg_log2, tpb = kCurBlock >> seg_log2;
   const int tl = static_cast<int>(threadIdx.x) & (tpb - 1);
-  const int seg = static_cast<int>(threadIdx.x) >> (8 - seg_log2);  // kCurBlock = 256
+  const int seg = static_cast<int>(threadIdx.x) >> (kCurBlockLog2 - seg_log2);
   const int per = (p.chunks + S - 1) >> seg_log2;
   const int c0 = seg * per, c1 = min(p.chunks, c0 + per);
   uint32_t *cnt = counts + static_cast<size_t>(bm) * p.chunks * p.tile_bound;
