@@ -422,9 +422,12 @@ __device__ __forceinline__ Tap make_tap(float loc_x, float loc_y, const Level &L
   t.x0 = x0;
   t.y0 = y0;
   t.in = in;
-  t.wx1 = ix - fx;
+  // a dropped sample's fractions are 0: its corners all read zero, and a NaN
+  // or infinite coordinate (ix - floor(ix) = NaN) would otherwise turn those
+  // zeros into NaN (NaN * 0); the reference kernel skips such a sample
+  t.wx1 = in ? ix - fx : 0.0f;
   t.wx0 = 1.0f - t.wx1;
-  t.wy1 = iy - fy;
+  t.wy1 = in ? iy - fy : 0.0f;
   t.wy0 = 1.0f - t.wy1;
   t.x0ok = in && x0 >= 0;
   t.x1ok = in && x0 + 1 < L.w;

@@ -305,6 +305,47 @@ def test_out_of_range_locations_give_zero(native_lib):
         assert torch.count_nonzero(x) == 0
 
 
+@pytest.mark.parametrize("path", ["one_call", "fused"])
+@pytest.mark.parametrize("value_dtype", [torch.float32, torch.bfloat16])
+def test_nan_locations_drop_the_sample(native_lib, path, value_dtype):
+    """A sample whose location has a NaN coordinate is dropped, as the
+    reference kernel's bounds test (h_im > -1 && ... false for NaN) drops it
+    (ms_deform_attn_musa_kernel.muh:289 forward, skipped samples' location
+    and weight gradients stored as 0 in the backward): it adds nothing to the
+    output or grad_value and gets zero location and weight gradients, while
+    every other sample matches the oracle. The oracle (grid_sample) would
+    give NaN gradients there, so it runs on the same inputs with those
+    samples' weights zeroed (and a finite stand-in location)."""
+    t, grad = small_case(11, 2, 37, 8, 32, ((10, 12), (5, 6), (3, 3), (2, 2)), 4)
+    g = torch.Generator().manual_seed(5)
+    loc = t["sampling_locations"]
+    drop = torch.rand(loc.shape[:-1], generator=g) < 0.1
+    which = torch.randint(0, 3, loc.shape[:-1], generator=g)  # NaN in x, y or both
+    loc[..., 0] = torch.where(drop & (which != 1), torch.nan, loc[..., 0])
+    loc[..., 1] = torch.where(drop & (which != 0), torch.nan, loc[..., 1])
+    geometry = torch.float32
+    if path == "one_call":
+        out = run_forward(native_lib, t, value_dtype, geometry)
+        gv, gl, ga = run_backward(native_lib, t, grad, value_dtype, geometry)
+    else:
+        out, gv, gl, ga = run_fused(native_lib, t, grad, value_dtype, geometry)
+    torch.cuda.synchronize()
+    masked = dict(t)
+    masked["sampling_locations"] = torch.where(drop[..., None], 0.5, loc)
+    masked["attention_weights"] = torch.where(drop, 0.0, t["attention_weights"])
+    o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
+        *oracle_inputs(masked, value_dtype, geometry), grad.to(value_dtype).float()
+    )
+    o_ga = torch.where(drop, 0.0, o_ga)  # dropped samples: zero weight gradient
+    ftol, btol = TOL[value_dtype]
+    _assert_close(out, o_out, ftol, "output")
+    _assert_close(gv, o_gv, btol, "grad_value")
+    _assert_close(gl, o_gl, btol, "grad_sampling_locations")
+    _assert_close(ga, o_ga, btol, "grad_attention_weights")
+    assert torch.count_nonzero(gl.cpu()[drop]) == 0
+    assert torch.count_nonzero(ga.cpu()[drop]) == 0
+
+
 @pytest.mark.parametrize("value_dtype", [torch.float32, torch.bfloat16])
 def test_half_pixel_known_answer_2048(native_lib, value_dtype):
     """Reference KAT (tests/ops/test_multi_scale_deformable_attn.py:430-468)."""
