@@ -308,7 +308,7 @@ def test_out_of_range_locations_give_zero(native_lib):
 @pytest.mark.parametrize("path", ["one_call", "fused"])
 @pytest.mark.parametrize("value_dtype", [torch.float32, torch.bfloat16])
 def test_nan_locations_drop_the_sample(native_lib, path, value_dtype):
-    """A sample whose location has a NaN coordinate is dropped, as the
+    """A sample whose location has a NaN (or infinite) coordinate is dropped, as the
     reference kernel's bounds test (h_im > -1 && ... false for NaN) drops it
     (ms_deform_attn_musa_kernel.muh:289 forward, skipped samples' location
     and weight gradients stored as 0 in the backward): it adds nothing to the
@@ -320,9 +320,13 @@ def test_nan_locations_drop_the_sample(native_lib, path, value_dtype):
     g = torch.Generator().manual_seed(5)
     loc = t["sampling_locations"]
     drop = torch.rand(loc.shape[:-1], generator=g) < 0.1
-    which = torch.randint(0, 3, loc.shape[:-1], generator=g)  # NaN in x, y or both
-    loc[..., 0] = torch.where(drop & (which != 1), torch.nan, loc[..., 0])
-    loc[..., 1] = torch.where(drop & (which != 0), torch.nan, loc[..., 1])
+    which = torch.randint(0, 3, loc.shape[:-1], generator=g)  # x, y or both
+    # NaN for most dropped samples, +inf or -inf for some
+    bad = torch.full(loc.shape[:-1], torch.nan)
+    kind = torch.randint(0, 4, loc.shape[:-1], generator=g)
+    bad = torch.where(kind == 2, torch.inf, torch.where(kind == 3, -torch.inf, bad))
+    loc[..., 0] = torch.where(drop & (which != 1), bad, loc[..., 0])
+    loc[..., 1] = torch.where(drop & (which != 0), bad, loc[..., 1])
     geometry = torch.float32
     if path == "one_call":
         out = run_forward(native_lib, t, value_dtype, geometry)
