@@ -350,6 +350,49 @@ def test_nan_locations_drop_the_sample(native_lib, path, value_dtype):
     assert torch.count_nonzero(ga.cpu()[drop]) == 0
 
 
+@pytest.mark.parametrize("path", ["one_call", "fused"])
+def test_value_past_2gib_takes_the_wide_paths(native_lib, path):
+    """A value tensor over 2 GiB: the row kernels and the tile backward address
+    value with 32-bit buffer offsets, so the host takes the generic forward
+    and the atomic backward (64-bit slab offsets), and the fused entry its
+    two-call fallback. Each batch entry's output and gradients depend on its
+    own value slab alone, so the oracle runs on a few entries, the last of
+    them past the 2 GiB mark."""
+    levels = ((32, 32), (16, 16), (8, 8), (4, 4))
+    batch, queries, heads, channels, points = 1600, 2, 8, 32, 4
+    nv = sum(h * w for h, w in levels)
+    assert batch * nv * heads * channels * 4 > 2**31
+    gen = torch.Generator(device=DEV).manual_seed(17)
+    L = len(levels)
+    t = {
+        "value": torch.randn(batch, nv, heads, channels, device=DEV, generator=gen),
+        "spatial_shapes": torch.tensor(levels, dtype=torch.int64),
+        "level_start_index": level_starts(levels),
+        "sampling_locations": torch.rand(batch, queries, heads, L, points, 2, device=DEV,
+                                         generator=gen) * 1.2 - 0.1,
+        "attention_weights": torch.softmax(
+            torch.randn(batch, queries, heads, L * points, device=DEV, generator=gen), -1
+        ).view(batch, queries, heads, L, points),
+    }
+    grad = torch.randn(batch, queries, heads * channels, device=DEV, generator=gen)
+    if path == "one_call":
+        out = run_forward(native_lib, t, torch.float32, torch.float32)
+        gv, gl, ga = run_backward(native_lib, t, grad, torch.float32, torch.float32)
+    else:
+        out, gv, gl, ga = run_fused(native_lib, t, grad, torch.float32, torch.float32)
+    torch.cuda.synchronize()
+    for b in (0, 777, batch - 1):
+        sl = slice(b, b + 1)
+        o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
+            t["value"][sl].cpu(), t["spatial_shapes"], t["sampling_locations"][sl].cpu(),
+            t["attention_weights"][sl].cpu(), grad[sl].cpu()
+        )
+        _assert_close(out[sl], o_out, 1e-5, f"output[{b}]")
+        _assert_close(gv[sl], o_gv, 1e-4, f"grad_value[{b}]")
+        _assert_close(gl[sl], o_gl, 1e-4, f"grad_sampling_locations[{b}]")
+        _assert_close(ga[sl], o_ga, 1e-4, f"grad_attention_weights[{b}]")
+
+
 @pytest.mark.parametrize("value_dtype", [torch.float32, torch.bfloat16])
 def test_half_pixel_known_answer_2048(native_lib, value_dtype):
     """Reference KAT (tests/ops/test_multi_scale_deformable_attn.py:430-468)."""
