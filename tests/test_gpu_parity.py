@@ -350,6 +350,40 @@ def test_nan_locations_drop_the_sample(native_lib, path, value_dtype):
     assert torch.count_nonzero(ga.cpu()[drop]) == 0
 
 
+def _random_case(seed):
+    """A seeded random shape: 1-3 batch entries, 1-300 queries, 1-8 heads,
+    channels for the row kernels (16, 32, 64) and the generic ones, 1-5
+    levels of 1-40 cells a side, 1-8 points, locations in [-0.2, 1.2]."""
+    r = torch.Generator().manual_seed(1000 + seed)
+    pick = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=r))
+    channels = (4, 8, 12, 16, 32, 64, 48, 32, 16)[pick(0, 8)]
+    levels = tuple((pick(1, 40), pick(1, 40)) for _ in range(pick(1, 5)))
+    case = (pick(1, 3), pick(1, 300), pick(1, 8), channels, levels, pick(1, 8))
+    return case, DTYPES[seed % len(DTYPES)]
+
+
+@pytest.mark.parametrize("path", ["one_call", "fused"])
+@pytest.mark.parametrize("seed", range(16))
+def test_random_shapes_match_oracle(native_lib, seed, path):
+    case, (value_dtype, geometry_dtype) = _random_case(seed)
+    t, grad = small_case(seed, *case, lo=-0.2, hi=1.2)
+    if path == "one_call":
+        out = run_forward(native_lib, t, value_dtype, geometry_dtype)
+        gv, gl, ga = run_backward(native_lib, t, grad, value_dtype, geometry_dtype)
+    else:
+        out, gv, gl, ga = run_fused(native_lib, t, grad, value_dtype, geometry_dtype)
+    torch.cuda.synchronize()
+    o_out, o_gv, o_gl, o_ga = msda_torch.msda_forward_backward(
+        *oracle_inputs(t, value_dtype, geometry_dtype), grad.to(value_dtype).float()
+    )
+    ftol, btol = TOL[value_dtype]
+    what = f"{_id(case)} {value_dtype}/{geometry_dtype}"
+    _assert_close(out, o_out, ftol, f"output {what}")
+    _assert_close(gv, o_gv, btol, f"grad_value {what}")
+    _assert_close(gl, o_gl, btol, f"grad_sampling_locations {what}")
+    _assert_close(ga, o_ga, btol, f"grad_attention_weights {what}")
+
+
 @pytest.mark.parametrize("path", ["one_call", "fused"])
 def test_value_past_2gib_takes_the_wide_paths(native_lib, path):
     """A value tensor over 2 GiB: the row kernels and the tile backward address
