@@ -17,6 +17,7 @@ from msda_testlib import scatter_div_case
 from muspace_amd import multi_scale_deformable_attn, multi_scale_deformable_attn_scatter_div
 from muspace_amd import workloads
 from oracle import msda_scatter_div
+from oracle.msda_torch import msda_forward
 
 pytestmark = [
     pytest.mark.gpu,
@@ -195,3 +196,76 @@ def test_more_cameras_than_one_launch_holds():
     (expected * g).sum().backward()
     for native, cpu in ((value, ref[0]), (loc, ref[2]), (attn, ref[3])):
         torch.testing.assert_close(native.grad.cpu(), cpu.grad, rtol=1e-4, atol=1e-4)
+
+
+_DTYPES = [(torch.float32, torch.float32), (torch.bfloat16, torch.float32),
+           (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32),
+           (torch.float16, torch.float16)]
+
+
+def _oracle_grads(ref, g, value_dtype):
+    """Oracle gradients for the grad rows the op hands the MSDA backward.
+
+    The op's backward gathers ``grad_slots[b, bev] * (1 / count[b, bev])`` into
+    per-camera rows stored in the value dtype (the rounding a 16-bit unfused
+    composition makes too), so the oracle's MSDA autograd is fed exactly those
+    rows; grad_slots passes through unchanged.
+    """
+    value, shapes, loc, attn, indexes, count, slots = ref
+    gq, inv = g.to(value_dtype).float(), 1.0 / count.detach()
+    rows, max_len = loc.shape[0], loc.shape[1]
+    cams, num_query = len(indexes), gq.shape[1]
+    grad_rows = torch.zeros(rows, max_len, gq.shape[-1])
+    for cam, index in enumerate(indexes):
+        keep = torch.nonzero((index >= 0) & (index < num_query)).flatten()
+        bev = index[keep]
+        for b in range(rows // cams):
+            grad_rows[b * cams + cam, keep] = (gq[b, bev] * inv[b, bev, None]).to(
+                value_dtype).float()
+    (msda_forward(value, shapes, loc, attn) * grad_rows).sum().backward()
+    return value.grad, loc.grad, attn.grad, gq
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_random_shapes_match_the_oracle(seed):
+    """Seeded random cameras, lengths, BEV sizes, levels, heads, points and
+    channels over every dtype combination; odd seeds turn 10% of the sampling
+    locations into NaN, which drops those samples (the oracle is given an
+    out-of-range location there instead)."""
+    r = torch.Generator().manual_seed(9000 + seed)
+    pick = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=r))  # noqa: E731
+    channels = (8, 16, 32, 64, 3, 32)[pick(0, 5)]
+    levels = tuple((pick(1, 20), pick(1, 20)) for _ in range(pick(1, 4)))
+    num_query = pick(4, 120)
+    case = scatter_div_case(seed, batch=pick(1, 3), cams=pick(2, 7),
+                            max_len=pick(2, num_query), num_query=num_query,
+                            heads=pick(1, 8), channels=channels, levels=levels,
+                            points=pick(1, 8), out_of_range=seed % 3 == 0)
+    value_dtype, geometry_dtype = _DTYPES[seed % len(_DTYPES)]
+    if seed % 2:
+        loc = case[3].clone()
+        drop = torch.rand(loc.shape[:-1], generator=r) < 0.1
+        loc[..., 1] = torch.where(drop, torch.nan, loc[..., 1])
+        case = case[:3] + (loc,) + case[4:]
+    dev = _device_case(case, value_dtype, geometry_dtype)
+    value, shapes, starts, loc, attn, indexes, count, slots = dev
+    for t in (value, loc, attn, slots):
+        t.requires_grad_(True)
+    ref = list(_oracle_inputs(dev))
+    ref[2] = torch.nan_to_num(ref[2], nan=-10.0)
+    ref = [t.clone().requires_grad_(t.is_floating_point()) if i != 4 else t
+           for i, t in enumerate(ref)]
+    out = multi_scale_deformable_attn_scatter_div(value, shapes, starts, loc, attn, indexes,
+                                                  count, slots.clone())
+    expected = msda_scatter_div.scatter_div(*[t.detach() if i != 4 else t
+                                              for i, t in enumerate(ref)])
+    fp32 = value_dtype == torch.float32
+    tol_f, tol_b = (1e-5, 1e-4) if fp32 else (2e-2, 2e-2)
+    torch.testing.assert_close(out.detach().float().cpu(), expected, rtol=tol_f, atol=tol_f)
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(seed))
+    (out.float() * g.to(DEV)).sum().backward()
+    for name, native, cpu in zip(("value", "loc", "attn", "slots"), (value, loc, attn, slots),
+                                 _oracle_grads(ref, g, value_dtype)):
+        assert native.grad.dtype == native.dtype
+        torch.testing.assert_close(native.grad.float().cpu(), cpu, rtol=tol_b, atol=tol_b,
+                                   msg=lambda m, name=name: f"{name}: {m}")
