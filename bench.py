@@ -682,9 +682,10 @@ def probe_library():
 
 
 def run_lds_atomic_probe() -> dict:
-    """fp32 against u32 LDS atomic adds (ds_add_f32 / ds_add_u32), conflict-
-    free and scattered addresses: clocks per wavefront instruction per CU,
-    at the device's reported clock."""
+    """fp32 against u32 and u64 LDS atomic adds (ds_add_f32 / ds_add_u32 /
+    ds_add_u64), consecutive (conflict-free for 32-bit) and scattered
+    addresses: clocks per wavefront instruction per CU, at the device's
+    reported clock."""
     lib = probe_library()
     props = torch.cuda.get_device_properties(0)
     cus = props.multi_processor_count
@@ -694,7 +695,8 @@ def run_lds_atomic_probe() -> dict:
     out = torch.empty(blocks * 1024, dtype=torch.int32, device="cuda")
     rows = {}
     for kind, name in ((0, "f32_conflict_free"), (1, "u32_conflict_free"),
-                       (2, "f32_scattered"), (3, "u32_scattered")):
+                       (2, "f32_scattered"), (3, "u32_scattered"),
+                       (5, "u64_consecutive"), (7, "u64_scattered")):
         def launch():
             rc = lib.muspace_probe_lds_atomic(out.data_ptr(), blocks, iters, kind, stream)
             assert rc == 0, rc

@@ -88,6 +88,50 @@ int row_slots(const dfa::Dims &d) {
   return C / dfa::kWave;
 }
 
+// Channel slice of dfa_backward_coarse (0: every map is left to the row
+// kernel's atomics), with its accumulator budget in cells and the bound on
+// contributions per sum (2^pair_log2 >= anchors * pts). The host does not see
+// the map sizes (device tensors), so it sizes the slice for the maps below the
+// finest of a pyramid that halves each scale, about a quarter of a camera's
+// rows: the widest slice whose accumulators hold that many cells. The kernels
+// choose the maps that fit on the device. The kernel reads grad_output in
+// 16-byte pieces and locations in 8-byte pieces, so it needs pointers aligned
+// to those.
+int coarse_slice(const dfa::Dims &d, const float *loc, const float *grad_out, int &budget,
+                 int &pair_log2) {
+  const int64_t pairs = static_cast<int64_t>(d.anchors) * d.pts;
+  if (d.scales == 0 || d.cams == 0 || pairs > (int64_t{1} << 20) ||
+      reinterpret_cast<uintptr_t>(grad_out) % 16 != 0 || reinterpret_cast<uintptr_t>(loc) % 8 != 0) {
+    return 0;
+  }
+  pair_log2 = 0;
+  while ((int64_t{1} << pair_log2) < pairs) ++pair_log2;
+  const int cpg = d.embeds / d.groups;
+  const int64_t want = static_cast<int64_t>(d.feat) / d.cams / 4;
+  for (int cs : {16, 8, 4}) {
+    if (cpg % cs != 0) continue;
+    budget = dfa::kCoarseLdsBytes / (8 * cs);
+    if (budget >= want || cs == 4) return cs;
+  }
+  return 0;
+}
+
+template <int CS>
+void launch_coarse(const int32_t *shape, const int32_t *start, const float *loc,
+                   const float *weights, const float *grad_out, float *grad_feat,
+                   const dfa::Dims &d, int budget, int pair_log2, hipStream_t st) {
+  const size_t lds = static_cast<size_t>(budget) * CS * sizeof(unsigned long long);
+  (void)hipFuncSetAttribute(reinterpret_cast<const void *>(dfa::dfa_backward_coarse<CS>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  // a workgroup takes up to four slices of one weight group
+  const int per_group = d.embeds / d.groups / CS;
+  int ns = 4;
+  while (per_group % ns != 0) --ns;
+  const int blocks = d.batch * d.cams * (d.embeds / (CS * ns));
+  dfa::dfa_backward_coarse<CS><<<blocks, dfa::kCoarseBlock, lds, st>>>(
+      shape, start, loc, weights, grad_out, grad_feat, d, budget, pair_log2, ns);
+}
+
 int forward_impl(const char *fn, bool optimized, const float *feat, const int32_t *shape,
                  const int32_t *start, const float *loc, const float *weights, float *out,
                  const DfaArgs &a, void *stream) {
@@ -146,22 +190,44 @@ int backward_impl(const char *fn, bool optimized, const float *feat, const int32
   const int blocks = (rows + dfa::kBlock / dfa::kWave - 1) / (dfa::kBlock / dfa::kWave);
   const uint32_t bytes = static_cast<uint32_t>(static_cast<uint64_t>(d.batch) * d.feat *
                                                d.embeds * 4u);
-  switch (nt) {
-    case 1:
-      dfa::dfa_backward_rows<1><<<blocks, dfa::kBlock, 0, st>>>(
-          feat, bytes, shape, start, loc, weights, grad_out, grad_feat, grad_loc, grad_weights, d);
+  // the small maps' feature gradients summed in LDS first (they only add)
+  int budget = 0, pair_log2 = 0;
+  const int cs = nt > 0 ? coarse_slice(d, loc, grad_out, budget, pair_log2) : 0;
+  switch (cs) {
+    case 16:
+      launch_coarse<16>(shape, start, loc, weights, grad_out, grad_feat, d, budget, pair_log2,
+                        st);
       break;
-    case 2:
-      dfa::dfa_backward_rows<2><<<blocks, dfa::kBlock, 0, st>>>(
-          feat, bytes, shape, start, loc, weights, grad_out, grad_feat, grad_loc, grad_weights, d);
-      break;
-    case 3:
-      dfa::dfa_backward_rows<3><<<blocks, dfa::kBlock, 0, st>>>(
-          feat, bytes, shape, start, loc, weights, grad_out, grad_feat, grad_loc, grad_weights, d);
+    case 8:
+      launch_coarse<8>(shape, start, loc, weights, grad_out, grad_feat, d, budget, pair_log2, st);
       break;
     case 4:
-      dfa::dfa_backward_rows<4><<<blocks, dfa::kBlock, 0, st>>>(
-          feat, bytes, shape, start, loc, weights, grad_out, grad_feat, grad_loc, grad_weights, d);
+      launch_coarse<4>(shape, start, loc, weights, grad_out, grad_feat, d, budget, pair_log2, st);
+      break;
+    default:
+      budget = 0;
+      break;
+  }
+  switch (nt) {
+    case 1:
+      dfa::dfa_backward_rows<1><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
+                                                                weights, grad_out, grad_feat,
+                                                                grad_loc, grad_weights, d, budget);
+      break;
+    case 2:
+      dfa::dfa_backward_rows<2><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
+                                                                weights, grad_out, grad_feat,
+                                                                grad_loc, grad_weights, d, budget);
+      break;
+    case 3:
+      dfa::dfa_backward_rows<3><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
+                                                                weights, grad_out, grad_feat,
+                                                                grad_loc, grad_weights, d, budget);
+      break;
+    case 4:
+      dfa::dfa_backward_rows<4><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
+                                                                weights, grad_out, grad_feat,
+                                                                grad_loc, grad_weights, d, budget);
       break;
     default:
       dfa::dfa_backward_generic<<<generic_blocks(static_cast<int64_t>(rows) * d.pts * d.cams),

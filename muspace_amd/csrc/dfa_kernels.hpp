@@ -28,6 +28,8 @@
 // Generic kernels (any C and groups) exist for shape coverage, not speed.
 #pragma once
 
+#include <cfloat>
+
 #include "msda_device.hpp"
 
 namespace dfa {
@@ -44,9 +46,11 @@ struct Dims {
 };
 
 // One (camera, scale) feature map; h = w = 0 marks a map that would reach
-// outside [0, num_feat) and is skipped instead of read out of bounds.
+// outside [0, num_feat) and is skipped instead of read out of bounds. lds:
+// the map's first accumulator cell in dfa_backward_coarse, or -1 when the
+// row kernel adds its feature gradients with device atomics.
 struct View {
-  int h, w, start;
+  int h, w, start, lds;
 };
 
 __device__ __forceinline__ void stage_views(View *v, const int32_t *shape, const int32_t *start,
@@ -56,7 +60,40 @@ __device__ __forceinline__ void stage_views(View *v, const int32_t *shape, const
     const int h = shape[2 * i], w = shape[2 * i + 1], s0 = start[i];
     const bool ok = h > 0 && w > 0 && s0 >= 0 &&
                     static_cast<int64_t>(s0) + static_cast<int64_t>(h) * w <= d.feat;
-    v[i] = ok ? View{h, w, s0} : View{0, 0, 0};
+    v[i] = ok ? View{h, w, s0, -1} : View{0, 0, 0, -1};
+  }
+  __syncthreads();
+}
+
+// Maps of one camera whose feature gradients dfa_backward_coarse sums in LDS:
+// the smallest maps first (ties: the lower scale) while their cells fit
+// `budget` in total. Sets View::lds of each chosen map and returns the cells
+// used. Both feature-gradient kernels run it on the same views, so they agree
+// on which maps the LDS kernel owns.
+__device__ inline int select_coarse(View *v, int scales, int budget) {
+  int used = 0;
+  for (;;) {
+    int best = -1, best_cells = 0;
+    for (int s = 0; s < scales; ++s) {
+      const int cells = v[s].h * v[s].w;  // 0 for a skipped map
+      if (v[s].lds < 0 && cells > 0 && (best < 0 || cells < best_cells)) {
+        best = s;
+        best_cells = cells;
+      }
+    }
+    if (best < 0 || best_cells > budget - used) break;
+    v[best].lds = used;
+    used += best_cells;
+  }
+  return used;
+}
+
+// select_coarse for every camera (budget 0: none), then a barrier.
+__device__ inline void mark_coarse(View *views, const Dims &d, int budget) {
+  if (budget > 0) {
+    for (int cam = threadIdx.x; cam < d.cams; cam += blockDim.x) {
+      select_coarse(views + cam * d.scales, d.scales, budget);
+    }
   }
   __syncthreads();
 }
@@ -182,10 +219,12 @@ __global__ void __launch_bounds__(kBlock)
                       const int32_t *__restrict__ shape, const int32_t *__restrict__ start,
                       const float *__restrict__ loc, const float *__restrict__ weights,
                       const float *__restrict__ grad_out, float *__restrict__ grad_feat,
-                      float *__restrict__ grad_loc, float *__restrict__ grad_weights, Dims d) {
+                      float *__restrict__ grad_loc, float *__restrict__ grad_weights, Dims d,
+                      int coarse_budget) {
   constexpr int C = NT * kWave;
   __shared__ View views[kMaxViews];
   stage_views(views, shape, start, d);
+  mark_coarse(views, d, coarse_budget);  // maps whose feature gradients another kernel sums
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int row = msda::xcd_logical_block(blockIdx.x, gridDim.x) * (kBlock / kWave) + wave;
   if (row >= d.batch * d.anchors) return;  // no barrier follows
@@ -261,9 +300,10 @@ __global__ void __launch_bounds__(kBlock)
           gy += static_cast<float>(v.h) * dh * top[t];
         }
         // feature gradient: one contiguous 256-byte atomic per corner and slot
+        // (maps summed by dfa_backward_coarse are left to it)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          if (ok[k]) {  // uniform across the wavefront
+          if (ok[k] && v.lds < 0) {  // uniform across the wavefront
             float *dst = grad_feat + batch_elem + static_cast<size_t>(v.start + tp.cell[k]) * C + lane;
 #pragma unroll
             for (int t = 0; t < NT; ++t) unsafeAtomicAdd(dst + t * kWave, tp.w[k] * top[t]);
@@ -300,6 +340,343 @@ __global__ void __launch_bounds__(kBlock)
       gl_row[2 * (base + lane)] = my_gx;
       gl_row[2 * (base + lane) + 1] = my_gy;
     }
+  }
+}
+
+// ------------------------------------------------------ coarse maps ---
+//
+// Feature gradients of a camera's small maps, summed in LDS. The row kernel
+// adds every corner contribution with an fp32 device atomic, and those
+// atomics bound it (all of them reach the memory side, ~330 G dwords/s). The
+// small maps take as many contributions as the large ones on far fewer cells,
+// so a workgroup per (batch entry, camera, run of channels) sums them in LDS,
+// CS channels at a time, and adds each cell once. fp32 LDS atomics cost ~194
+// clocks per wavefront instruction on gfx950 and 64-bit integer ones 8-14, so
+// the sums are fixed point: contribution x = w_corner * (grad_out * weight)
+// becomes the integer nearest x * 2^S (an exact float64 product rounded once
+// by a fused multiply-add against 1.5 * 2^52, whose low mantissa bits then
+// hold the integer). S is chosen per workgroup from a bound on |x| (the
+// largest |grad_out| of its channels times the largest weight of its maps,
+// both over its active pairs; bilinear weights are at most 1) so that no sum
+// of at most 2^pair_log2 contributions passes 2^50: |x| < 2^e gives
+// S = 50 - pair_log2 - e. The integer sums are exact and independent of
+// order; each contribution is rounded by at most 2^-(S+1), about
+// 2^-(51 - pair_log2) of the bound. A workgroup that meets a non-finite
+// grad_out or weight adds with fp32 device atomics instead, as the row kernel
+// would.
+
+constexpr int kCoarseBlock = 1024;
+constexpr int kCoarseLdsBytes = 128 * 1024;  // accumulators of one workgroup
+constexpr int kCoarseList = 4096;            // active pairs listed in LDS
+constexpr int kCoarseUnroll = 4;             // locations per thread per listing step
+
+// Grid: batch * cams * (C / (CS * ns)) workgroups (runs of ns slices of CS
+// channels inside one weight group; run fastest, XCD-contiguous, so an XCD
+// serves whole batch entries from its L2); dynamic LDS: budget * CS 64-bit
+// sums. The workgroup lists its active (anchor, pt) pairs in LDS and holds
+// their locations and weights in registers (up to kPer a thread); then, per
+// slice, one thread per pair adds every LDS map, corner and channel, and the
+// workgroup adds the sums to grad_feat.
+template <int CS>
+__global__ void __launch_bounds__(kCoarseBlock)
+    dfa_backward_coarse(const int32_t *__restrict__ shape, const int32_t *__restrict__ start,
+                        const float *__restrict__ loc, const float *__restrict__ weights,
+                        const float *__restrict__ grad_out, float *__restrict__ grad_feat,
+                        Dims d, int budget, int pair_log2, int ns) {
+  static_assert(CS == 4 || CS == 8 || CS == 16, "slices of 4, 8 or 16 channels");
+  extern __shared__ unsigned long long acc[];
+  __shared__ View views[kMaxViews];
+  __shared__ int coarse[kMaxViews];      // the camera's LDS maps (scale indices), by View::lds
+  __shared__ int shared_map[kMaxViews];  // 1: the map overlaps another map (atomic adds)
+  __shared__ int list[kCoarseList];      // active pairs
+  __shared__ int n_coarse, n_used, n_list;
+  __shared__ uint32_t max_w_bits, max_g_bits;
+  __shared__ int any_bad;
+  stage_views(views, shape, start, d);
+  mark_coarse(views, d, budget);
+  const int C = d.embeds, runs = C / (CS * ns);
+  const int lb = msda::xcd_logical_block(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));
+  const int run = lb % runs, cam = (lb / runs) % d.cams, b = lb / (runs * d.cams);
+  const View *cv = views + cam * d.scales;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  if (tid == 0) {  // the LDS maps in accumulator order
+    int n = 0, used = 0;
+    for (int s = 0; s < d.scales; ++s) {
+      if (cv[s].lds < 0) continue;
+      int at = n++;
+      for (; at > 0 && cv[coarse[at - 1]].lds > cv[s].lds; --at) coarse[at] = coarse[at - 1];
+      coarse[at] = s;
+      used += cv[s].h * cv[s].w;
+    }
+    for (int i = 0; i < n; ++i) shared_map[i] = 0;
+    for (int s = n; s < 4; ++s) coarse[s] = 0;  // read (not used) by the unrolled weight loads
+    n_coarse = n;
+    n_used = used;
+    n_list = 0;
+    max_w_bits = 0u;
+    max_g_bits = 0u;
+    any_bad = 0;
+  }
+  __syncthreads();
+  const int nsc = n_coarse, used = n_used;
+  if (nsc == 0) return;  // uniform: the camera has no LDS map
+  // an LDS map that overlaps another map is added to grad_feat atomically
+  const int nviews = d.cams * d.scales;
+  for (int t = tid; t < nsc * nviews; t += blockDim.x) {
+    const int i = t / nviews, j = t - i * nviews;
+    const View &m = cv[coarse[i]];
+    const int64_t lo = m.start, hi = lo + static_cast<int64_t>(m.h) * m.w;
+    const int64_t olo = views[j].start, ohi = olo + static_cast<int64_t>(views[j].h) * views[j].w;
+    if (j != cam * d.scales + coarse[i] && ohi > olo && olo < hi && lo < ohi) shared_map[i] = 1;
+  }
+  for (int i = tid; i < used * CS; i += blockDim.x) acc[i] = 0ull;
+
+  const int ch0 = run * ns * CS;  // first channel of the run
+  const int group = ch0 / (C / d.groups);
+  const int sg = d.scales * d.groups;
+  const int pairs = d.anchors * d.pts;  // (anchor, pt) pairs of this (batch entry, camera)
+  const size_t row0 = static_cast<size_t>(b) * d.anchors;
+  auto pair_index = [&](int p) {  // index of (b, anchor, pt, cam) in loc and weights
+    const int a = p / d.pts;
+    return ((row0 + a) * d.pts + (p - a * d.pts)) * d.cams + cam;
+  };
+  auto grad_at = [&](int p, int ch) {  // grad_out of the pair's anchor from channel ch
+    return reinterpret_cast<const float4 *>(grad_out + (row0 + p / d.pts) * C + ch);
+  };
+  auto load_weights = [&](int p, float (&w)[4]) {
+    const float *wp = weights + pair_index(p) * sg + group;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = i < nsc ? wp[coarse[i] * d.groups] : 0.0f;
+  };
+  float mw = 0.0f, mg = 0.0f;
+  bool bad = false;
+  auto bound_pair = [&](int p, const float (&w)[4]) {  // weights, then the run's grad_out
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = fabsf(w[i]);
+      bad |= !(a <= FLT_MAX);
+      mw = fmaxf(mw, a);
+    }
+    for (int i = 4; i < nsc; ++i) {  // more than four LDS maps: the rest from memory
+      const float a = fabsf(weights[pair_index(p) * sg + group + coarse[i] * d.groups]);
+      bad |= !(a <= FLT_MAX);
+      mw = fmaxf(mw, a);
+    }
+    const float4 *go = grad_at(p, ch0);
+    for (int q = 0; q < ns * CS / 4; ++q) {
+      const float4 g = go[q];
+      const float a = fmaxf(fmaxf(fabsf(g.x), fabsf(g.y)), fmaxf(fabsf(g.z), fabsf(g.w)));
+      // fmaxf drops NaN, so each component is tested
+      bad |= !(fabsf(g.x) <= FLT_MAX && fabsf(g.y) <= FLT_MAX && fabsf(g.z) <= FLT_MAX &&
+               fabsf(g.w) <= FLT_MAX);
+      mg = fmaxf(mg, a);
+    }
+  };
+
+  // 1. list the active pairs (locations only)
+  for (int p0 = 0; p0 < pairs; p0 += kCoarseUnroll * kCoarseBlock) {
+    float2 xy[kCoarseUnroll];
+#pragma unroll
+    for (int j = 0; j < kCoarseUnroll; ++j) {
+      const int p = min(p0 + j * kCoarseBlock + tid, pairs - 1);
+      xy[j] = *reinterpret_cast<const float2 *>(loc + 2 * pair_index(p));
+    }
+#pragma unroll
+    for (int j = 0; j < kCoarseUnroll; ++j) {
+      const int p = p0 + j * kCoarseBlock + tid;
+      const bool act = p < pairs && active(xy[j].x, xy[j].y);
+      const uint64_t m = __ballot(act);
+      int base = 0;
+      if (lane == 0 && m != 0) base = atomicAdd(&n_list, __popcll(m));
+      base = __shfl(base, 0, kWave);
+      const int slot =
+          base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                           __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+      if (act && slot < kCoarseList) list[slot] = p;
+    }
+  }
+  __syncthreads();
+  const int listed = n_list;
+
+  // 2. the listed pairs' locations and weights into registers (when they fit)
+  // and the bound over them; past that, over every active pair from memory
+  constexpr int kPer = CS == 4 ? 3 : CS == 8 ? 2 : 1;
+  static_assert(kPer * kCoarseBlock <= kCoarseList, "held pairs come from the list");
+  const bool in_regs = listed <= kPer * kCoarseBlock;
+  int pp[kPer];
+  float2 pxy[kPer];
+  float pw[kPer][4];
+  if (in_regs) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = tid + j * kCoarseBlock;
+      pp[j] = i < listed ? list[i] : -1;
+      if (pp[j] >= 0) {
+        pxy[j] = *reinterpret_cast<const float2 *>(loc + 2 * pair_index(pp[j]));
+        load_weights(pp[j], pw[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      if (pp[j] >= 0) bound_pair(pp[j], pw[j]);
+    }
+  } else {
+    for (int p = tid; p < pairs; p += blockDim.x) {
+      const float2 xy = *reinterpret_cast<const float2 *>(loc + 2 * pair_index(p));
+      if (!active(xy.x, xy.y)) continue;
+      float w[4];
+      load_weights(p, w);
+      bound_pair(p, w);
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    mw = fmaxf(mw, __shfl_xor(mw, off, kWave));
+    mg = fmaxf(mg, __shfl_xor(mg, off, kWave));
+  }
+  const bool wave_bad = __ballot(bad) != 0;
+  if (lane == 0) {  // non-negative floats order as their bit patterns
+    atomicMax(&max_w_bits, __float_as_uint(mw));
+    atomicMax(&max_g_bits, __float_as_uint(mg));
+    if (wave_bad) any_bad = 1;
+  }
+  __syncthreads();
+  const float bound = __uint_as_float(max_g_bits) * __uint_as_float(max_w_bits);
+  const bool slow = any_bad != 0 || !(bound <= FLT_MAX);
+  if (!slow && bound == 0.0f) return;  // uniform: every contribution is zero
+  int e2 = 0;
+  (void)frexpf(bound, &e2);  // bound < 2^e2
+  const int shift = 50 - pair_log2 - e2;
+  const double scale = ldexp(1.0, shift), inv_scale = ldexp(1.0, -shift);
+  constexpr double kMagic = 6755399441055744.0;  // 1.5 * 2^52
+  const long long magic_bits = __double_as_longlong(kMagic);
+  const size_t feat_b = static_cast<size_t>(b) * d.feat;
+  int map_end[4];  // accumulator ends of the first four maps
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    map_end[i] = i < nsc ? (cv[coarse[i]].lds + cv[coarse[i]].h * cv[coarse[i]].w) * CS : INT_MAX;
+  }
+
+  // 3. every LDS map, corner and channel of one active pair in slice `ch`
+  auto add_pair = [&](int p, float2 xy, const float (&g)[CS], const float (&w)[4], int ch) {
+    for (int si = 0; si < nsc; ++si) {
+      const View v = cv[coarse[si]];
+      const float wg = si == 0   ? w[0]
+                       : si == 1 ? w[1]
+                       : si == 2 ? w[2]
+                       : si == 3 ? w[3]
+                                 : weights[pair_index(p) * sg + group + coarse[si] * d.groups];
+      const Tap tp = make_tap(xy.x, xy.y, v);
+      if (slow) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (tp.cell[k] < 0) continue;
+          float *dst = grad_feat + (feat_b + v.start + tp.cell[k]) * C + ch;
+#pragma unroll
+          for (int c = 0; c < CS; ++c) unsafeAtomicAdd(dst + c, tp.w[k] * (g[c] * wg));
+        }
+        continue;
+      }
+      double wk[4];
+      int at[4];  // first accumulator of the corner's cell, -1 outside the map
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        wk[k] = tp.w[k];
+        at[k] = tp.cell[k] >= 0 ? (v.lds + tp.cell[k]) * CS : -1;
+      }
+#pragma unroll
+      for (int c = 0; c < CS; ++c) {
+        const double tc = static_cast<double>(g[c] * wg) * scale;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (at[k] < 0) continue;
+          const long long q = __double_as_longlong(fma(wk[k], tc, kMagic)) - magic_bits;
+          atomicAdd(acc + at[k] + c, static_cast<unsigned long long>(q));
+        }
+      }
+    }
+  };
+  auto load_grad = [&](int p, int ch, float (&g)[CS]) {
+    const float4 *go = grad_at(p, ch);
+#pragma unroll
+    for (int q = 0; q < CS / 4; ++q) {
+      const float4 v = go[q];
+      g[4 * q] = v.x;
+      g[4 * q + 1] = v.y;
+      g[4 * q + 2] = v.z;
+      g[4 * q + 3] = v.w;
+    }
+  };
+
+  for (int sl = 0; sl < ns; ++sl) {
+    const int ch = ch0 + sl * CS;
+    if (in_regs) {
+      float pg[kPer][CS];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        if (pp[j] >= 0) load_grad(pp[j], ch, pg[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        if (pp[j] >= 0) add_pair(pp[j], pxy[j], pg[j], pw[j], ch);
+      }
+    } else {
+      for (int p = tid; p < pairs; p += blockDim.x) {
+        const float2 xy = *reinterpret_cast<const float2 *>(loc + 2 * pair_index(p));
+        if (!active(xy.x, xy.y)) continue;
+        float g[CS], w[4];
+        load_weights(p, w);
+        load_grad(p, ch, g);
+        add_pair(p, xy, g, w, ch);
+      }
+    }
+    if (slow) continue;  // uniform
+    __syncthreads();
+    // 4. the sums into grad_feat; each accumulator is cleared for the next
+    // slice once read. The accumulators are the LDS maps' cells back to back;
+    // a thread reads kFlush of them together, so their grad_feat reads
+    // overlap. Element offsets fit 32 bits: the row kernels address the
+    // feature tensor with 32-bit byte offsets.
+    constexpr int kFlush = 8;
+    for (int i0 = 0; i0 < used * CS; i0 += kFlush * kCoarseBlock) {
+      float old[kFlush], add[kFlush];
+      uint32_t off[kFlush];
+      uint32_t own = 0u;  // bit j: no other map shares element j's row
+#pragma unroll
+      for (int j = 0; j < kFlush; ++j) {
+        const int i = i0 + j * kCoarseBlock + tid;
+        long long q = 0;
+        if (i < used * CS) {
+          q = static_cast<long long>(acc[i]);
+          acc[i] = 0ull;
+        }
+        add[j] = static_cast<float>(static_cast<double>(q) * inv_scale);
+        int si = 0;  // the map of accumulator i
+        if (nsc > 4) {
+          while (si + 1 < nsc &&
+                 i >= (cv[coarse[si]].lds + cv[coarse[si]].h * cv[coarse[si]].w) * CS) {
+            ++si;
+          }
+        } else {
+          si = (i >= map_end[0]) + (i >= map_end[1]) + (i >= map_end[2]);
+        }
+        const View &v = cv[coarse[si]];
+        off[j] = static_cast<uint32_t>((feat_b + v.start + (i / CS - v.lds)) * C + ch + i % CS);
+        const bool mine = shared_map[si] == 0;
+        own |= mine ? 1u << j : 0u;
+        old[j] = mine && q != 0 ? grad_feat[off[j]] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < kFlush; ++j) {
+        if (add[j] == 0.0f) continue;
+        if ((own >> j) & 1u) {
+          grad_feat[off[j]] = old[j] + add[j];  // the only writer of this element in this kernel
+        } else {
+          unsafeAtomicAdd(grad_feat + off[j], add[j]);
+        }
+      }
+    }
+    __syncthreads();
   }
 }
 

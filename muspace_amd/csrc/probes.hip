@@ -87,6 +87,23 @@ __device__ __forceinline__ void lds_atomic_body(T *out, int iters, bool scattere
   out[blockIdx.x * blockDim.x + threadIdx.x] = s[t];
 }
 
+// 64-bit integer adds (ds_add_u64) into an 8192-entry array (64 KB); out[]
+// gets the low word of one entry per thread.
+__global__ void __launch_bounds__(1024)
+    probe_lds_atomic64(uint32_t *out, int iters, bool scattered) {
+  __shared__ unsigned long long s[8192];
+  for (int i = threadIdx.x; i < 8192; i += blockDim.x) s[i] = 0ull;
+  __syncthreads();
+  const uint32_t t = threadIdx.x;
+  for (int it = 0; it < iters; ++it) {
+    const uint32_t a = scattered ? mix(t * 8191u + static_cast<uint32_t>(it)) & 8191u
+                                 : (t + 97u * static_cast<uint32_t>(it)) & 8191u;
+    atomicAdd(&s[a], 1ull);
+  }
+  __syncthreads();
+  out[blockIdx.x * blockDim.x + threadIdx.x] = static_cast<uint32_t>(s[t]);
+}
+
 __global__ void __launch_bounds__(1024) probe_lds_atomic(uint32_t *out, int iters, int kind) {
   if (kind & 1) {
     lds_atomic_body<uint32_t>(out, iters, (kind & 2) != 0);
@@ -129,14 +146,21 @@ __attribute__((visibility("default"))) int muspace_probe_atomic(float *buf, uint
 }
 
 // blocks workgroups of 1024 threads, each thread `iters` LDS atomic adds
-// (kind as probe_lds_atomic); out: blocks * 1024 words. Returns a hipError_t.
+// (kind 0-3 as probe_lds_atomic; 5 and 7: 64-bit integer adds, consecutive
+// and scattered); out: blocks * 1024 words. Returns a hipError_t.
 __attribute__((visibility("default"))) int muspace_probe_lds_atomic(uint32_t *out, int blocks,
                                                                     int iters, int kind,
                                                                     void *stream) {
-  if (out == nullptr || blocks <= 0 || iters <= 0 || kind < 0 || kind > 3) {
+  if (out == nullptr || blocks <= 0 || iters <= 0 || kind < 0 || kind > 7 || kind == 4 ||
+      kind == 6) {
     return hipErrorInvalidValue;
   }
-  probe_lds_atomic<<<blocks, 1024, 0, static_cast<hipStream_t>(stream)>>>(out, iters, kind);
+  if (kind & 4) {
+    probe_lds_atomic64<<<blocks, 1024, 0, static_cast<hipStream_t>(stream)>>>(out, iters,
+                                                                              (kind & 2) != 0);
+  } else {
+    probe_lds_atomic<<<blocks, 1024, 0, static_cast<hipStream_t>(stream)>>>(out, iters, kind);
+  }
   return hipGetLastError();
 }
 

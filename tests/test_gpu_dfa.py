@@ -256,3 +256,78 @@ def test_backward_twice_with_a_smaller_case():
         torch.testing.assert_close(gf.cpu().double(), ef, rtol=1e-4, atol=1e-4)
         torch.testing.assert_close(gl.cpu().double(), el, **LOC_TOL)
         torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4)
+
+
+# --- the coarse maps' LDS sums (dfa_backward_coarse) -------------------------------------------
+# The optimised backward sums the feature gradients of each camera's small maps in LDS as
+# fixed-point integers, with a scale chosen per workgroup from the largest contribution; a
+# workgroup that meets a non-finite grad_output or weight falls back to fp32 device atomics.
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e30])
+def test_coarse_sums_keep_their_precision_at_any_gradient_scale(scale):
+    """grad_output scaled by 1e-30 and 1e30: the fixed-point scale follows, so the feature
+    and weight gradients keep the 1e-4 relative bar."""
+    case = _medium_case(21, 256, 8, anchors=120)
+    grad_out = torch.randn(2, 120, 256, generator=torch.Generator().manual_seed(22)) * scale
+    gf, gl, gw = _backward_opt(case, grad_out)
+    ef, el, ew = _oracle_grads(case, grad_out)
+    assert torch.isfinite(gf).all()
+    torch.testing.assert_close(gf.cpu().double(), ef, rtol=1e-4, atol=1e-4 * scale)
+    torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4 * scale)
+
+
+def test_non_finite_grad_output_matches_the_base_kernels():
+    """An inf and a NaN in grad_output: the workgroups that see them add with fp32 atomics,
+    so every gradient equals the base kernels' (non-finite entries included)."""
+    lib = load_native_module()
+    case = _medium_case(23, 256, 8, anchors=80)
+    grad_out = torch.randn(2, 80, 256, generator=torch.Generator().manual_seed(24))
+    grad_out[0, 5, 40] = float("inf")
+    grad_out[1, 9, 3] = float("nan")
+    mc, spatial, start, loc, weights = _to_device(case, requires_grad=False)
+    results = []
+    for name in ("opt", "base"):
+        gf, gl, gw = torch.zeros_like(mc), torch.zeros_like(loc), torch.zeros_like(weights)
+        getattr(lib, f"deformable_aggregation_backward_{name}")(mc, spatial, start, loc, weights,
+                                                                grad_out.to(DEV), gf, gl, gw)
+        results.append((gf, gl, gw))
+    assert not torch.isfinite(results[0][0]).all()
+    for a, b, tol in zip(*results, (dict(rtol=1e-4, atol=1e-4), LOC_TOL,
+                                    dict(rtol=1e-4, atol=1e-4))):
+        torch.testing.assert_close(a, b, equal_nan=True, **tol)
+
+
+def test_every_point_active_matches_the_base_kernels():
+    """SparseDrive's shape with every (anchor, point, camera) inside its image: 11,700 active
+    pairs per (batch entry, camera), more than a workgroup lists or holds, so the coarse
+    kernel reads its pairs from memory."""
+    lib = load_native_module()
+    t = make_dfa_inputs(seed=31, device=DEV, active_frac=1.0)
+    mc, spatial, start, loc, weights = (t[k] for k in ("mc_ms_feat", "spatial_shape",
+                                                        "scale_start_index",
+                                                        "sampling_location", "weights"))
+    results = []
+    for name in ("opt", "base"):
+        gf, gl, gw = torch.zeros_like(mc), torch.zeros_like(loc), torch.zeros_like(weights)
+        getattr(lib, f"deformable_aggregation_backward_{name}")(mc, spatial, start, loc, weights,
+                                                                t["grad_output"], gf, gl, gw)
+        results.append((gf, gl, gw))
+    for a, b, tol in zip(*results, (dict(rtol=1e-4, atol=1e-4), LOC_TOL,
+                                    dict(rtol=1e-4, atol=1e-4))):
+        torch.testing.assert_close(a, b, **tol)
+
+
+def test_more_than_four_small_maps():
+    """Six maps per camera, all small enough for LDS: the maps past the fourth take their
+    weights from memory."""
+    case = list(random_case(25, batch=2, anchors=70, pts=4, cams=2,
+                            shapes=((12, 16), (8, 10), (6, 8), (4, 5), (3, 3), (2, 2)),
+                            channels=128, groups=4))
+    case[3].copy_(torch.round(case[3] * 4096) / 4096)
+    grad_out = torch.randn(2, 70, 128, generator=torch.Generator().manual_seed(26))
+    gf, gl, gw = _backward_opt(case, grad_out)
+    ef, el, ew = _oracle_grads(case, grad_out)
+    torch.testing.assert_close(gf.cpu().double(), ef, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(gl.cpu().double(), el, **LOC_TOL)
+    torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4)
