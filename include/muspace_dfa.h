@@ -42,6 +42,12 @@
  *    multiple of 64 up to 256 with power-of-two group widths, else the generic
  *    kernels; _base always runs the generic kernels (one thread per output
  *    element forward, per (batch, anchor, pt, cam) backward).
+ *  - backward_opt (row-kernel layout, num_anchors * num_pts <= 2^20, 16-byte
+ *    aligned grad_output, 8-byte aligned sampling_location) first sums the
+ *    feature gradients of each camera's smallest maps in LDS as 64-bit
+ *    fixed-point integers scaled from a bound on the contributions, then adds
+ *    them once per cell; those sums are deterministic. A non-finite
+ *    grad_output or weight sends the affected workgroup to fp32 atomics.
  */
 #ifndef MUSPACE_DFA_H_
 #define MUSPACE_DFA_H_

@@ -373,10 +373,12 @@ constexpr int kCoarseUnroll = 4;             // locations per thread per listing
 // Grid: batch * cams * (C / (CS * ns)) workgroups (runs of ns slices of CS
 // channels inside one weight group; run fastest, XCD-contiguous, so an XCD
 // serves whole batch entries from its L2); dynamic LDS: budget * CS 64-bit
-// sums. The workgroup lists its active (anchor, pt) pairs in LDS and holds
-// their locations and weights in registers (up to kPer a thread); then, per
-// slice, one thread per pair adds every LDS map, corner and channel, and the
-// workgroup adds the sums to grad_feat.
+// sums, channel-major (acc[c * cells + cell]: the lanes of one add, each on a
+// random cell, then spread over the banks). The workgroup lists its active
+// (anchor, pt) pairs in LDS and holds their locations and weights in
+// registers (up to kPer a thread); then, per slice, one thread per pair adds
+// every LDS map, corner and channel, and the workgroup adds the sums to
+// grad_feat.
 template <int CS>
 __global__ void __launch_bounds__(kCoarseBlock)
     dfa_backward_coarse(const int32_t *__restrict__ shape, const int32_t *__restrict__ start,
@@ -578,11 +580,11 @@ __global__ void __launch_bounds__(kCoarseBlock)
         continue;
       }
       double wk[4];
-      int at[4];  // first accumulator of the corner's cell, -1 outside the map
+      int at[4];  // accumulator cell of the corner, -1 outside the map
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         wk[k] = tp.w[k];
-        at[k] = tp.cell[k] >= 0 ? (v.lds + tp.cell[k]) * CS : -1;
+        at[k] = tp.cell[k] >= 0 ? v.lds + tp.cell[k] : -1;
       }
 #pragma unroll
       for (int c = 0; c < CS; ++c) {
@@ -591,7 +593,7 @@ __global__ void __launch_bounds__(kCoarseBlock)
         for (int k = 0; k < 4; ++k) {
           if (at[k] < 0) continue;
           const long long q = __double_as_longlong(fma(wk[k], tc, kMagic)) - magic_bits;
-          atomicAdd(acc + at[k] + c, static_cast<unsigned long long>(q));
+          atomicAdd(acc + c * used + at[k], static_cast<unsigned long long>(q));
         }
       }
     }
@@ -646,9 +648,10 @@ __global__ void __launch_bounds__(kCoarseBlock)
       for (int j = 0; j < kFlush; ++j) {
         const int i = i0 + j * kCoarseBlock + tid;
         long long q = 0;
-        if (i < used * CS) {
-          q = static_cast<long long>(acc[i]);
-          acc[i] = 0ull;
+        if (i < used * CS) {  // channel-major in LDS: acc[c * used + cell]
+          const int a = (i % CS) * used + i / CS;
+          q = static_cast<long long>(acc[a]);
+          acc[a] = 0ull;
         }
         add[j] = static_cast<float>(static_cast<double>(q) * inv_scale);
         int si = 0;  // the map of accumulator i
