@@ -213,7 +213,7 @@ struct TileBinner {
 // binning the chunk's samples as it goes (TileBinner). Grid: slabs x chunks
 // blocks, logical blocks contiguous per XCD.
 template <typename VT, typename GT, int C, int NS, int T>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kBlock, kRowWavesPerSimd)
     msda_forward_bin_rows(const VT *__restrict__ value, uint32_t value_bytes,
                           const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                           const GT *__restrict__ loc, const GT *__restrict__ attn,
@@ -233,7 +233,7 @@ __global__ void __launch_bounds__(kBlock)
 // plans whose units are one step each (the host checks), where a sample's
 // probability is final when its tap is computed.
 template <typename VT, typename GT, int C, int NS, int T>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kBlock, kRowWavesPerSimd)
     msda_forward_softmax_bin_rows(const VT *__restrict__ value, uint32_t value_bytes,
                                   const int64_t *__restrict__ shapes,
                                   const int64_t *__restrict__ starts, const GT *__restrict__ loc,

@@ -27,6 +27,11 @@
 namespace msda {
 
 constexpr int kBlock = 256;  // 4 wavefronts
+// The forward row kernels are built for two of their blocks per CU (two
+// wavefronts per SIMD), so at most 256 registers a lane: past that (even one
+// register kept in an AGPR) gfx950 allocates the next granule and a SIMD holds
+// one wavefront. The launch bound makes the compiler keep to it.
+constexpr int kRowWavesPerSimd = 2;
 
 // Launch geometry of the row kernels, computed on the host.
 struct RowPlan {
@@ -549,7 +554,7 @@ __device__ __forceinline__ void forward_rows(const VT *__restrict__ value, uint3
 }
 
 template <typename VT, typename GT, int C, int NS>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kBlock, kRowWavesPerSimd)
     msda_forward_rows(const VT *__restrict__ value, uint32_t value_bytes,
                       const int64_t *__restrict__ shapes, const int64_t *__restrict__ starts,
                       const GT *__restrict__ loc, const GT *__restrict__ attn,
@@ -562,7 +567,7 @@ __global__ void __launch_bounds__(kBlock)
 // Forward with the attention weights given as logits: softmax over each
 // unit's L*P samples fused into the prologue (forward_rows, kSoftmax).
 template <typename VT, typename GT, int C, int NS>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kBlock, kRowWavesPerSimd)
     msda_forward_softmax_rows(const VT *__restrict__ value, uint32_t value_bytes,
                               const int64_t *__restrict__ shapes,
                               const int64_t *__restrict__ starts, const GT *__restrict__ loc,
@@ -578,7 +583,7 @@ __global__ void __launch_bounds__(kBlock)
 // (CameraSlots above); s.batch is the batch. Each camera's units take the
 // logical blocks [out.blk[j], out.blk[j+1]).
 template <typename VT, typename GT, int C, int NS, bool kAtomic>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kBlock, kRowWavesPerSimd)
     msda_forward_scatter_div_rows(const VT *__restrict__ value, uint32_t value_bytes,
                                   const int64_t *__restrict__ shapes,
                                   const int64_t *__restrict__ starts, const GT *__restrict__ loc,
@@ -756,7 +761,7 @@ __device__ __forceinline__ void forward_generic(const VT *__restrict__ value,
 }
 
 template <typename VT, typename GT>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kBlock, kRowWavesPerSimd)
     msda_forward_generic(const VT *__restrict__ value, const int64_t *__restrict__ shapes,
                          const int64_t *__restrict__ starts, const GT *__restrict__ loc,
                          const GT *__restrict__ attn, VT *__restrict__ out, Shape s) {
@@ -764,7 +769,7 @@ __global__ void __launch_bounds__(kBlock)
 }
 
 template <typename VT, typename GT, bool kAtomic>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kBlock, kRowWavesPerSimd)
     msda_forward_scatter_div_generic(const VT *__restrict__ value,
                                      const int64_t *__restrict__ shapes,
                                      const int64_t *__restrict__ starts,
