@@ -468,9 +468,9 @@ __global__ void __launch_bounds__(kCoarseBlock)
     for (int q = 0; q < ns * CS / 4; ++q) {
       const float4 g = go[q];
       const float a = fmaxf(fmaxf(fabsf(g.x), fabsf(g.y)), fmaxf(fabsf(g.z), fabsf(g.w)));
-      // fmaxf drops NaN, so each component is tested
-      bad |= !(fabsf(g.x) <= FLT_MAX && fabsf(g.y) <= FLT_MAX && fabsf(g.z) <= FLT_MAX &&
-               fabsf(g.w) <= FLT_MAX);
+      // fmaxf drops NaN (an inf stays in a); a NaN component makes the sum NaN
+      const float sum = (g.x + g.y) + (g.z + g.w);
+      bad |= !(a <= FLT_MAX) || sum != sum;
       mg = fmaxf(mg, a);
     }
   };
