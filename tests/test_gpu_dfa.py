@@ -331,3 +331,27 @@ def test_more_than_four_small_maps():
     torch.testing.assert_close(gf.cpu().double(), ef, rtol=1e-4, atol=1e-4)
     torch.testing.assert_close(gl.cpu().double(), el, **LOC_TOL)
     torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4)
+
+
+def test_misaligned_grad_output_and_locations_skip_the_coarse_kernel():
+    """grad_output 4 bytes past a 16-byte boundary and locations 4 bytes past an 8-byte one:
+    the backward leaves the coarse kernel out (it reads them in 16- and 8-byte pieces) and
+    every map takes the row kernel's atomics; the gradients are the aligned call's."""
+    lib = load_native_module()
+    case = _medium_case(27, 256, 8, anchors=50)
+    mc, spatial, start, loc, weights = _to_device(case, requires_grad=False)
+    grad_out = torch.randn(2, 50, 256, generator=torch.Generator().manual_seed(28)).to(DEV)
+    shifted_go = torch.empty(grad_out.numel() + 1, device=DEV)[1:].view_as(grad_out)
+    shifted_go.copy_(grad_out)
+    shifted_loc = torch.empty(loc.numel() + 1, device=DEV)[1:].view_as(loc)
+    shifted_loc.copy_(loc)
+    assert shifted_go.data_ptr() % 16 == 4 and shifted_loc.data_ptr() % 8 == 4
+    results = []
+    for go, lc in ((grad_out, loc), (shifted_go, loc), (grad_out, shifted_loc)):
+        gf, gl, gw = torch.zeros_like(mc), torch.zeros_like(loc), torch.zeros_like(weights)
+        lib.deformable_aggregation_backward_opt(mc, spatial, start, lc, weights, go, gf, gl, gw)
+        results.append((gf, gl, gw))
+    for other in results[1:]:
+        for a, b, tol in zip(results[0], other, (dict(rtol=1e-4, atol=1e-4), LOC_TOL,
+                                                 dict(rtol=1e-4, atol=1e-4))):
+            torch.testing.assert_close(b, a, **tol)
