@@ -337,20 +337,25 @@ def harness_ms(fn, warmup: int = 20, iterations: int = 100, repeats: int = 5) ->
     return statistics.median(samples)
 
 
-def _event_ms(fn, steps: int, warmup: int) -> float:
-    """Mean ms of fn() over `steps` calls, HIP events on the current stream."""
+def _event_ms(fn, steps: int, warmup: int, repeats: int = 3) -> float:
+    """ms of fn() per call, HIP events on the current stream: the median over
+    `repeats` timed runs of `steps` calls each (one stalled run, such as a
+    first allocation inside it, does not set the figure)."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        fn()
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    runs = []
+    for _ in range(repeats):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
+        runs.append(start.elapsed_time(end) / steps)
+    return statistics.median(runs)
 
 
 def time_sca(lib, steps: int = 50, warmup: int = 10) -> dict:
