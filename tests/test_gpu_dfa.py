@@ -355,3 +355,34 @@ def test_misaligned_grad_output_and_locations_skip_the_coarse_kernel():
         for a, b, tol in zip(results[0], other, (dict(rtol=1e-4, atol=1e-4), LOC_TOL,
                                                  dict(rtol=1e-4, atol=1e-4))):
             torch.testing.assert_close(b, a, **tol)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes_backward_matches_the_oracle(seed):
+    """Seeded random channels (64-256), group widths (8 lanes to two 64-channel slots), 1-5
+    maps of up to 40 x 40 per camera, 1-6 cameras, up to 300 anchors and 13 points, grad_output
+    scaled by 1e-3 to 1e3 (the coarse kernel's fixed-point scale follows it), every third seed
+    with 10% NaN locations."""
+    r = torch.Generator().manual_seed(11000 + seed)
+    pick = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=r))  # noqa: E731
+    channels = (64, 128, 192, 256)[pick(0, 3)]
+    widths = [c for c in (8, 16, 32, 64, 128)
+              if channels % c == 0 and channels // c <= 8 and (c < 64 or c % 64 == 0)]
+    groups = channels // widths[pick(0, len(widths) - 1)]
+    shapes = tuple((pick(1, 40), pick(1, 40)) for _ in range(pick(1, 5)))
+    cams, anchors, pts = pick(1, 6), pick(1, 300), pick(2, 13)
+    case = list(random_case(seed, batch=pick(1, 3), anchors=anchors, pts=pts, cams=cams,
+                            shapes=shapes, channels=channels, groups=groups))
+    loc = case[3]
+    loc.copy_(torch.round(loc * 4096) / 4096)
+    if seed % 3 == 0:
+        drop = torch.rand(loc.shape[:-1], generator=r) < 0.1
+        loc[..., 0] = torch.where(drop, torch.nan, loc[..., 0])
+    scale = 10.0 ** pick(-3, 3)
+    grad_out = torch.randn(case[0].shape[0], anchors, channels,
+                           generator=torch.Generator().manual_seed(seed)) * scale
+    gf, gl, gw = _backward_opt(case, grad_out)
+    ef, el, ew = _oracle_grads(case, grad_out)
+    torch.testing.assert_close(gf.cpu().double(), ef, rtol=1e-4, atol=1e-4 * scale)
+    torch.testing.assert_close(gl.cpu().double(), el, rtol=1e-4, atol=1e-3 * scale)
+    torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4 * scale)
