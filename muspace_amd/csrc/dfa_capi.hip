@@ -187,7 +187,12 @@ int backward_impl(const char *fn, bool optimized, const float *feat, const int32
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nt = optimized ? row_slots(d) : 0;
   const int rows = d.batch * d.anchors;
-  const int blocks = (rows + dfa::kBlock / dfa::kWave - 1) / (dfa::kBlock / dfa::kWave);
+  // wavefronts per row of dfa_backward_rows: few rows give each of the 1024
+  // SIMDs few wavefronts with long serial pair walks, so a row's pairs are
+  // shared (SparseDrive's 7,200 rows: four per row measured fastest)
+  const int parts = rows >= 8192 * 4 ? 1 : rows >= 8192 * 2 ? 2 : 4;
+  const int units = nt > 0 ? rows * parts : rows;
+  const int blocks = (units + dfa::kBlock / dfa::kWave - 1) / (dfa::kBlock / dfa::kWave);
   const uint32_t bytes = static_cast<uint32_t>(static_cast<uint64_t>(d.batch) * d.feat *
                                                d.embeds * 4u);
   // the small maps' feature gradients summed in LDS first (they only add)
@@ -212,22 +217,26 @@ int backward_impl(const char *fn, bool optimized, const float *feat, const int32
     case 1:
       dfa::dfa_backward_rows<1><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
                                                                 weights, grad_out, grad_feat,
-                                                                grad_loc, grad_weights, d, budget);
+                                                                grad_loc, grad_weights, d, budget,
+                                                                parts);
       break;
     case 2:
       dfa::dfa_backward_rows<2><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
                                                                 weights, grad_out, grad_feat,
-                                                                grad_loc, grad_weights, d, budget);
+                                                                grad_loc, grad_weights, d, budget,
+                                                                parts);
       break;
     case 3:
       dfa::dfa_backward_rows<3><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
                                                                 weights, grad_out, grad_feat,
-                                                                grad_loc, grad_weights, d, budget);
+                                                                grad_loc, grad_weights, d, budget,
+                                                                parts);
       break;
     case 4:
       dfa::dfa_backward_rows<4><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
                                                                 weights, grad_out, grad_feat,
-                                                                grad_loc, grad_weights, d, budget);
+                                                                grad_loc, grad_weights, d, budget,
+                                                                parts);
       break;
     default:
       dfa::dfa_backward_generic<<<generic_blocks(static_cast<int64_t>(rows) * d.pts * d.cams),

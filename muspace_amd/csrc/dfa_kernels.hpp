@@ -213,6 +213,16 @@ __global__ void __launch_bounds__(kBlock)
   for (int t = 0; t < NT; ++t) o[t * kWave] += acc[t];
 }
 
+// Backward, one (batch, anchor) row split over `parts` wavefronts: the row's
+// active pairs are dealt round-robin (by their rank among the active pairs)
+// so that every wavefront of the row gets a near-equal share; a skipped
+// pair's zero gradients go to the wavefront `pair % parts`. Location and
+// weight gradients are per pair and feature gradients are atomics, so the
+// parts need no reduction. A pair's corner rows and weights are loaded two
+// scales at a time before either is used, so one memory latency covers two
+// scales (four scales at once cost registers and occupancy: slower).
+constexpr int kScaleRun = 2;
+
 template <int NT>
 __global__ void __launch_bounds__(kBlock)
     dfa_backward_rows(const float *__restrict__ feat, uint32_t feat_bytes,
@@ -220,13 +230,14 @@ __global__ void __launch_bounds__(kBlock)
                       const float *__restrict__ loc, const float *__restrict__ weights,
                       const float *__restrict__ grad_out, float *__restrict__ grad_feat,
                       float *__restrict__ grad_loc, float *__restrict__ grad_weights, Dims d,
-                      int coarse_budget) {
+                      int coarse_budget, int parts) {
   constexpr int C = NT * kWave;
   __shared__ View views[kMaxViews];
   stage_views(views, shape, start, d);
   mark_coarse(views, d, coarse_budget);  // maps whose feature gradients another kernel sums
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int row = msda::xcd_logical_block(blockIdx.x, gridDim.x) * (kBlock / kWave) + wave;
+  const int unit = msda::xcd_logical_block(blockIdx.x, gridDim.x) * (kBlock / kWave) + wave;
+  const int row = unit / parts, part = unit % parts;
   if (row >= d.batch * d.anchors) return;  // no barrier follows
   const int b = row / d.anchors;
   const int cpg = C / d.groups;
@@ -248,17 +259,27 @@ __global__ void __launch_bounds__(kBlock)
   float *gl_row = grad_loc + static_cast<size_t>(row) * pairs * 2;
   float *gw_row = grad_weights + static_cast<size_t>(row) * pairs * sg;
   const size_t batch_elem = static_cast<size_t>(b) * d.feat * C;
+  const uint32_t batch_row = static_cast<uint32_t>(b) * static_cast<uint32_t>(d.feat);
+  const uint64_t below = (uint64_t{1} << lane) - 1;
+  int seen = 0;  // active pairs of the row before this run of 64
   for (int base = 0; base < pairs; base += kWave) {
     const int n = min(kWave, pairs - base);
     const int pi = base + min(lane, n - 1);
     const float lx = loc_row[2 * pi], ly = loc_row[2 * pi + 1];
-    const uint64_t act = __ballot(lane < n && active(lx, ly));
+    const bool on = lane < n && active(lx, ly);
+    const uint64_t act = __ballot(on);
+    const int owner = on ? (seen + __builtin_popcountll(act & below)) % parts : pi % parts;
+    const uint64_t own = __ballot(lane < n && owner == part);
+    seen += __builtin_popcountll(act);
     // weight gradients of skipped pairs are zero
     for (int e = lane; e < n * sg; e += kWave) {
-      if (!((act >> (e / sg)) & 1)) gw_row[static_cast<size_t>(base) * sg + e] = 0.0f;
+      const int p = e / sg;
+      if (!((act >> p) & 1) && (base + p) % parts == part) {
+        gw_row[static_cast<size_t>(base) * sg + e] = 0.0f;
+      }
     }
     float my_gx = 0.0f, my_gy = 0.0f;  // location gradient of this lane's pair
-    uint64_t mask = act;
+    uint64_t mask = act & own;
     while (mask) {
       const int l = __builtin_ctzll(mask);
       mask &= mask - 1;
@@ -267,64 +288,80 @@ __global__ void __launch_bounds__(kBlock)
       const int pair = base + l, cam = pair % d.cams;
       const float *wp = w_row + static_cast<size_t>(pair) * sg;
       float *gwp = gw_row + static_cast<size_t>(pair) * sg;
+      const View *cv = views + cam * d.scales;
       float gx = 0.0f, gy = 0.0f;
-      for (int s = 0; s < d.scales; ++s) {
-        const View v = views[cam * d.scales + s];
-        const Tap tp = make_tap(x, y, v);
-        float val[4][NT];
-        bool ok[4];
+      for (int s0 = 0; s0 < d.scales; s0 += kScaleRun) {
+        // every load of the run first (scales past the last read nothing)
+        float val[kScaleRun][4][NT];
+        float wv[kScaleRun][NT];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          ok[k] = v.h > 0 && tp.cell[k] >= 0;
-          const uint32_t row_off =
-              ok[k] ? (static_cast<uint32_t>(b) * static_cast<uint32_t>(d.feat) +
-                       static_cast<uint32_t>(v.start + tp.cell[k])) * (C * 4u)
-                    : kOobOffset;
+        for (int j = 0; j < kScaleRun; ++j) {
+          const int s = min(s0 + j, d.scales - 1);
+          const View v = cv[s];
+          const Tap tp = make_tap(x, y, v);
 #pragma unroll
-          for (int t = 0; t < NT; ++t) val[k][t] = buffer_load4(rf, row_off + (t * kWave + lane) * 4u);
-        }
-        float gwt[NT];
-        float top[NT];
+          for (int k = 0; k < 4; ++k) {
+            const bool ok = s0 + j < d.scales && v.h > 0 && tp.cell[k] >= 0;
+            const uint32_t row_off =
+                ok ? (batch_row + static_cast<uint32_t>(v.start + tp.cell[k])) * (C * 4u)
+                   : kOobOffset;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          const float wg = wp[s * d.groups + grp[t]];
-          top[t] = g[t] * wg;
-          const float sampled = tp.w[0] * val[0][t] + tp.w[1] * val[1][t] +
-                                tp.w[2] * val[2][t] + tp.w[3] * val[3][t];
-          gwt[t] = g[t] * sampled;
-          const float dh = -tp.hw * val[0][t] - tp.lw * val[1][t] + tp.hw * val[2][t] +
-                           tp.lw * val[3][t];
-          const float dw = -tp.hh * val[0][t] + tp.hh * val[1][t] - tp.lh * val[2][t] +
-                           tp.lh * val[3][t];
-          gx += static_cast<float>(v.w) * dw * top[t];
-          gy += static_cast<float>(v.h) * dh * top[t];
-        }
-        // feature gradient: one contiguous 256-byte atomic per corner and slot
-        // (maps summed by dfa_backward_coarse are left to it)
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          if (ok[k] && v.lds < 0) {  // uniform across the wavefront
-            float *dst = grad_feat + batch_elem + static_cast<size_t>(v.start + tp.cell[k]) * C + lane;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) unsafeAtomicAdd(dst + t * kWave, tp.w[k] * top[t]);
+            for (int t = 0; t < NT; ++t) {
+              val[j][k][t] = buffer_load4(rf, row_off + (t * kWave + lane) * 4u);
+            }
           }
+#pragma unroll
+          for (int t = 0; t < NT; ++t) wv[j][t] = wp[s * d.groups + grp[t]];
         }
-        // weight gradient of each group: sum over its channels
-        if (tpg == 1) {
+#pragma unroll
+        for (int j = 0; j < kScaleRun; ++j) {
+          const int s = s0 + j;
+          if (s >= d.scales) break;  // uniform
+          const View v = cv[s];
+          const Tap tp = make_tap(x, y, v);
+          float gwt[NT];
+          float top[NT];
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
-            const float sum = segment_sum(gwt[t], seg);
-            if ((lane & (seg - 1)) == 0) gwp[s * d.groups + grp[t]] = sum;
+            top[t] = g[t] * wv[j][t];
+            const float q0 = val[j][0][t], q1 = val[j][1][t], q2 = val[j][2][t],
+                        q3 = val[j][3][t];
+            gwt[t] = g[t] * (tp.w[0] * q0 + tp.w[1] * q1 + tp.w[2] * q2 + tp.w[3] * q3);
+            const float dh = -tp.hw * q0 - tp.lw * q1 + tp.hw * q2 + tp.lw * q3;
+            const float dw = -tp.hh * q0 + tp.hh * q1 - tp.lh * q2 + tp.lh * q3;
+            gx += static_cast<float>(v.w) * dw * top[t];
+            gy += static_cast<float>(v.h) * dh * top[t];
           }
-        } else {
+          // feature gradient: one contiguous 256-byte atomic per corner and slot
+          // (maps summed by dfa_backward_coarse are left to it)
+          if (v.lds < 0 && v.h > 0) {  // uniform across the wavefront
 #pragma unroll
-          for (int t = 0; t < NT; ++t) gwt[t] = wave_sum(gwt[t]);
-          if (lane == 0) {
-            for (int gi = 0; gi < d.groups; ++gi) {
-              float sum = 0.0f;
+            for (int k = 0; k < 4; ++k) {
+              if (tp.cell[k] >= 0) {
+                float *dst =
+                    grad_feat + batch_elem + static_cast<size_t>(v.start + tp.cell[k]) * C + lane;
 #pragma unroll
-              for (int t = 0; t < NT; ++t) sum += t / tpg == gi ? gwt[t] : 0.0f;
-              gwp[s * d.groups + gi] = sum;
+                for (int t = 0; t < NT; ++t) unsafeAtomicAdd(dst + t * kWave, tp.w[k] * top[t]);
+              }
+            }
+          }
+          // weight gradient of each group: sum over its channels
+          if (tpg == 1) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+              const float sum = segment_sum(gwt[t], seg);
+              if ((lane & (seg - 1)) == 0) gwp[s * d.groups + grp[t]] = sum;
+            }
+          } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) gwt[t] = wave_sum(gwt[t]);
+            if (lane == 0) {
+              for (int gi = 0; gi < d.groups; ++gi) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) sum += t / tpg == gi ? gwt[t] : 0.0f;
+                gwp[s * d.groups + gi] = sum;
+              }
             }
           }
         }
@@ -336,7 +373,7 @@ __global__ void __launch_bounds__(kBlock)
         my_gy = gy;
       }
     }
-    if (lane < n) {
+    if ((own >> lane) & 1) {
       gl_row[2 * (base + lane)] = my_gx;
       gl_row[2 * (base + lane) + 1] = my_gy;
     }
