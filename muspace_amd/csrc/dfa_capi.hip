@@ -145,25 +145,30 @@ int forward_impl(const char *fn, bool optimized, const float *feat, const int32_
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nt = optimized ? row_slots(d) : 0;
   const int rows = d.batch * d.anchors;
-  const int blocks = (rows + dfa::kBlock / dfa::kWave - 1) / (dfa::kBlock / dfa::kWave);
+  // wavefronts per row of dfa_forward_rows (1, 2 or 4: one workgroup holds a
+  // row's parts): few rows give each SIMD few wavefronts with long serial
+  // pair walks, so a row's pairs are shared
+  const int parts = rows >= 8192 * 4 ? 1 : rows >= 8192 * 2 ? 2 : 4;
+  const int units = nt > 0 ? rows * parts : rows;
+  const int blocks = (units + dfa::kBlock / dfa::kWave - 1) / (dfa::kBlock / dfa::kWave);
   const uint32_t bytes = static_cast<uint32_t>(static_cast<uint64_t>(d.batch) * d.feat *
                                                d.embeds * 4u);
   switch (nt) {
     case 1:
       dfa::dfa_forward_rows<1><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
-                                                               weights, out, d);
+                                                               weights, out, d, parts);
       break;
     case 2:
       dfa::dfa_forward_rows<2><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
-                                                               weights, out, d);
+                                                               weights, out, d, parts);
       break;
     case 3:
       dfa::dfa_forward_rows<3><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
-                                                               weights, out, d);
+                                                               weights, out, d, parts);
       break;
     case 4:
       dfa::dfa_forward_rows<4><<<blocks, dfa::kBlock, 0, st>>>(feat, bytes, shape, start, loc,
-                                                               weights, out, d);
+                                                               weights, out, d, parts);
       break;
     default:
       dfa::dfa_forward_generic<<<generic_blocks(static_cast<int64_t>(rows) * d.embeds),

@@ -17,12 +17,12 @@
 // (/root/reference/csrc/deformable_aggregation/deformable_aggregation_musa.mu:39-160,304-430)
 // and the PyTorch reference (/root/reference/mu_space/ops/deformable_aggregation.py:88-158).
 //
-// Row kernels (C = 64*NT channels, NT <= 4): one wavefront per (batch, anchor);
-// lane i owns channels i, i+64, ... so every gather, atomic and store of a
-// corner row is a contiguous 256-byte access. The lanes load the locations of
-// 64 (pt, cam) pairs at once and ballot the active ones; the wavefront then
-// walks only the active pairs, whose geometry is uniform (read from the owning
-// lane). Corner loads are unconditional raw buffer loads: a corner outside its
+// Row kernels (C = 64*NT channels, NT <= 4): one to four wavefronts per
+// (batch, anchor) row; lane i owns channels i, i+64, ... so every gather,
+// atomic and store of a corner row is a contiguous 256-byte access. The lanes
+// load the locations of 64 (pt, cam) pairs at once and ballot the active ones;
+// each wavefront then walks only its share of the active pairs, whose geometry
+// is uniform (read from the owning lane). Corner loads are unconditional raw buffer loads: a corner outside its
 // map gets an out-of-range offset, which reads zero.
 //
 // Generic kernels (any C and groups) exist for shape coverage, not speed.
@@ -148,19 +148,25 @@ __device__ __forceinline__ float segment_sum(float v, int width) {
   return v;
 }
 
+// Forward, one (batch, anchor) row over `parts` (1, 2 or 4) wavefronts of one
+// workgroup: the row's active pairs are dealt round-robin by their rank among
+// the active pairs, and the parts' partial rows are summed through LDS by
+// part 0, which adds the row to `out`.
 template <int NT>
 __global__ void __launch_bounds__(kBlock)
     dfa_forward_rows(const float *__restrict__ feat, uint32_t feat_bytes,
                      const int32_t *__restrict__ shape, const int32_t *__restrict__ start,
                      const float *__restrict__ loc, const float *__restrict__ weights,
-                     float *__restrict__ out, Dims d) {
+                     float *__restrict__ out, Dims d, int parts) {
   constexpr int C = NT * kWave;
   __shared__ View views[kMaxViews];
+  __shared__ float partial[kBlock / kWave][C];
   stage_views(views, shape, start, d);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int row = msda::xcd_logical_block(blockIdx.x, gridDim.x) * (kBlock / kWave) + wave;
-  if (row >= d.batch * d.anchors) return;  // no barrier follows
-  const int b = row / d.anchors;
+  const int unit = msda::xcd_logical_block(blockIdx.x, gridDim.x) * (kBlock / kWave) + wave;
+  const int row = unit / parts, part = unit % parts;
+  const bool live = row < d.batch * d.anchors;  // every wavefront reaches the barrier below
+  const int b = live ? row / d.anchors : 0;
   const int cpg = C / d.groups;
   const __amdgpu_buffer_rsrc_t rf = msda::make_rsrc(feat, feat_bytes);
   int grp[NT];
@@ -174,10 +180,16 @@ __global__ void __launch_bounds__(kBlock)
   const float *loc_row = loc + static_cast<size_t>(row) * pairs * 2;
   const float *w_row = weights + static_cast<size_t>(row) * pairs * sg;
   const uint32_t batch_base = static_cast<uint32_t>(b) * static_cast<uint32_t>(d.feat);
-  for (int base = 0; base < pairs; base += kWave) {
+  const uint64_t below = (uint64_t{1} << lane) - 1;
+  int seen = 0;  // active pairs of the row before this run of 64
+  for (int base = 0; live && base < pairs; base += kWave) {
     const int pi = min(base + lane, pairs - 1);
     const float lx = loc_row[2 * pi], ly = loc_row[2 * pi + 1];
-    uint64_t mask = __ballot(base + lane < pairs && active(lx, ly));
+    const bool on = base + lane < pairs && active(lx, ly);
+    const uint64_t act = __ballot(on);
+    const bool mine = on && (seen + __builtin_popcountll(act & below)) % parts == part;
+    seen += __builtin_popcountll(act);
+    uint64_t mask = __ballot(mine);
     while (mask) {
       const int l = __builtin_ctzll(mask);
       mask &= mask - 1;
@@ -208,6 +220,19 @@ __global__ void __launch_bounds__(kBlock)
       }
     }
   }
+  if (parts > 1) {  // uniform over the workgroup
+    if (part > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) partial[wave][t * kWave + lane] = acc[t];
+    }
+    __syncthreads();
+    if (part > 0) return;
+    for (int w = wave + 1; w < wave + parts; ++w) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] += partial[w][t * kWave + lane];
+    }
+  }
+  if (!live) return;
   float *o = out + static_cast<size_t>(row) * C + lane;
 #pragma unroll
   for (int t = 0; t < NT; ++t) o[t * kWave] += acc[t];
