@@ -333,6 +333,35 @@ def test_more_than_four_small_maps():
     torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("rows", [16384, 32768])
+def test_row_counts_past_the_split_thresholds_match_the_base_kernels(rows):
+    """The row kernels share a row's pairs among four wavefronts below 16,384 (batch, anchor)
+    rows, two below 32,768 and one from there on; every other test stays below 16,384. At the
+    two larger counts, forward and backward against the base kernels."""
+    lib = load_native_module()
+    batch = 2
+    anchors = rows // batch
+    case = list(random_case(rows, batch=batch, anchors=anchors, pts=3, cams=3,
+                            shapes=((12, 20), (6, 10), (3, 5)), channels=256, groups=8,
+                            dtype=torch.float32))
+    case[3].copy_(torch.round(case[3] * 4096) / 4096)
+    grad_out = torch.randn(batch, anchors, 256, generator=torch.Generator().manual_seed(rows))
+    mc, spatial, start, loc, weights = _to_device(case, requires_grad=False)
+    outs = []
+    for name in ("opt", "base"):
+        out = torch.zeros((batch, anchors, 256), device=DEV)
+        getattr(lib, f"deformable_aggregation_forward_{name}")(mc, spatial, start, loc, weights,
+                                                               out)
+        gf, gl, gw = torch.zeros_like(mc), torch.zeros_like(loc), torch.zeros_like(weights)
+        getattr(lib, f"deformable_aggregation_backward_{name}")(mc, spatial, start, loc, weights,
+                                                                grad_out.to(DEV), gf, gl, gw)
+        outs.append((out, gf, gl, gw))
+    assert outs[1][0].abs().max() > 0 and outs[1][1].abs().max() > 0
+    for a, b, tol in zip(*outs, (dict(rtol=1e-5, atol=1e-5), dict(rtol=1e-4, atol=1e-4),
+                                 LOC_TOL, dict(rtol=1e-4, atol=1e-4))):
+        torch.testing.assert_close(a, b, **tol)
+
+
 def test_misaligned_grad_output_and_locations_skip_the_coarse_kernel():
     """grad_output 4 bytes past a 16-byte boundary and locations 4 bytes past an 8-byte one:
     the backward leaves the coarse kernel out (it reads them in 16- and 8-byte pieces) and
