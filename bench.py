@@ -561,8 +561,8 @@ def cpu_baseline() -> dict:
     reference's PyTorch path) on the host CPU with every available core:
     c0 forward only at full size; c1-c3 forward + autograd backward in float32
     and c4 in float32 on value-upcast inputs, each on a query subset scaled to
-    the full query count. Protocol of the survey's CPU plan: warmup 1, then 3
-    repeats of 3 iterations, median of the repeats' per-call seconds."""
+    the full query count. Protocol: warmup 1, then 3 repeats of 3 iterations,
+    median of the repeats' per-call seconds."""
     from oracle import msda_torch
 
     threads = cpu_threads()
