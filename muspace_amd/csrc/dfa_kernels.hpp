@@ -136,16 +136,14 @@ __device__ __forceinline__ float buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
+// Sum over the wavefront, every lane receiving it (DPP inside the 16-lane
+// rows, readlane across them: no LDS-routed shuffles). Whole wavefront active.
+__device__ __forceinline__ float wave_sum(float v) { return msda::group_sum_sel(v, kWave); }
 
-// Sum over aligned runs of `width` lanes (a power of two <= 64).
+// Sum over aligned runs of `width` lanes (a power of two <= 64, uniform),
+// every lane of the run receiving it; whole wavefront active.
 __device__ __forceinline__ float segment_sum(float v, int width) {
-  for (int off = 1; off < width; off <<= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  return msda::group_sum_sel(v, width);
 }
 
 // Forward, one (batch, anchor) row over `parts` (1, 2 or 4) wavefronts of one
@@ -164,7 +162,7 @@ __global__ void __launch_bounds__(kBlock)
   stage_views(views, shape, start, d);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int unit = msda::xcd_logical_block(blockIdx.x, gridDim.x) * (kBlock / kWave) + wave;
-  const int row = unit / parts, part = unit % parts;
+  const int row = unit / parts, part = unit & (parts - 1);  // parts: 1, 2 or 4
   const bool live = row < d.batch * d.anchors;  // every wavefront reaches the barrier below
   const int b = live ? row / d.anchors : 0;
   const int cpg = C / d.groups;
@@ -187,7 +185,7 @@ __global__ void __launch_bounds__(kBlock)
     const float lx = loc_row[2 * pi], ly = loc_row[2 * pi + 1];
     const bool on = base + lane < pairs && active(lx, ly);
     const uint64_t act = __ballot(on);
-    const bool mine = on && (seen + __builtin_popcountll(act & below)) % parts == part;
+    const bool mine = on && ((seen + __builtin_popcountll(act & below)) & (parts - 1)) == part;
     seen += __builtin_popcountll(act);
     uint64_t mask = __ballot(mine);
     while (mask) {
@@ -262,7 +260,7 @@ __global__ void __launch_bounds__(kBlock)
   mark_coarse(views, d, coarse_budget);  // maps whose feature gradients another kernel sums
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int unit = msda::xcd_logical_block(blockIdx.x, gridDim.x) * (kBlock / kWave) + wave;
-  const int row = unit / parts, part = unit % parts;
+  const int row = unit / parts, part = unit & (parts - 1);  // parts: 1, 2 or 4
   if (row >= d.batch * d.anchors) return;  // no barrier follows
   const int b = row / d.anchors;
   const int cpg = C / d.groups;
@@ -286,6 +284,9 @@ __global__ void __launch_bounds__(kBlock)
   const size_t batch_elem = static_cast<size_t>(b) * d.feat * C;
   const uint32_t batch_row = static_cast<uint32_t>(b) * static_cast<uint32_t>(d.feat);
   const uint64_t below = (uint64_t{1} << lane) - 1;
+  const int sgd = sg > 0 ? sg : 1;  // no scales: nothing is zeroed
+  const int lane_p = lane / sgd, lane_j = lane - lane_p * sgd;  // element `lane` of a run
+  const int step_p = kWave / sgd, step_j = kWave - step_p * sgd;
   int seen = 0;  // active pairs of the row before this run of 64
   for (int base = 0; base < pairs; base += kWave) {
     const int n = min(kWave, pairs - base);
@@ -293,14 +294,20 @@ __global__ void __launch_bounds__(kBlock)
     const float lx = loc_row[2 * pi], ly = loc_row[2 * pi + 1];
     const bool on = lane < n && active(lx, ly);
     const uint64_t act = __ballot(on);
-    const int owner = on ? (seen + __builtin_popcountll(act & below)) % parts : pi % parts;
+    const int owner = (on ? seen + __builtin_popcountll(act & below) : pi) & (parts - 1);
     const uint64_t own = __ballot(lane < n && owner == part);
     seen += __builtin_popcountll(act);
-    // weight gradients of skipped pairs are zero
-    for (int e = lane; e < n * sg; e += kWave) {
-      const int p = e / sg;
-      if (!((act >> p) & 1) && (base + p) % parts == part) {
+    // weight gradients of skipped pairs are zero: element e = p * sg + j of
+    // the run, (p, j) stepped by kWave elements per pass (no division inside)
+    for (int e = lane, p = lane_p, j = lane_j; e < n * sg; e += kWave) {
+      if (!((act >> p) & 1) && ((base + p) & (parts - 1)) == part) {
         gw_row[static_cast<size_t>(base) * sg + e] = 0.0f;
+      }
+      p += step_p;
+      j += step_j;
+      if (j >= sg) {
+        j -= sg;
+        ++p;
       }
     }
     float my_gx = 0.0f, my_gy = 0.0f;  // location gradient of this lane's pair
