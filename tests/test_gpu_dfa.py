@@ -333,13 +333,14 @@ def test_more_than_four_small_maps():
     torch.testing.assert_close(gw.cpu().double(), ew, rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("rows", [16384, 32768])
+@pytest.mark.parametrize("rows", [16384, 16385, 32768])
 def test_row_counts_past_the_split_thresholds_match_the_base_kernels(rows):
     """The row kernels share a row's pairs among four wavefronts below 16,384 (batch, anchor)
     rows, two below 32,768 and one from there on; every other test stays below 16,384. At the
-    two larger counts, forward and backward against the base kernels."""
+    two larger counts, forward and backward against the base kernels; an odd count leaves the
+    last workgroup of the two-wavefront split with a row and two idle wavefronts."""
     lib = load_native_module()
-    batch = 2
+    batch = 2 if rows % 2 == 0 else 1
     anchors = rows // batch
     case = list(random_case(rows, batch=batch, anchors=anchors, pts=3, cams=3,
                             shapes=((12, 20), (6, 10), (3, 5)), channels=256, groups=8,
