@@ -680,6 +680,9 @@ def probe_library():
                                          ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     lib.muspace_probe_atomic.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_void_p]
+    lib.muspace_probe_scatter.restype = ctypes.c_int
+    lib.muspace_probe_scatter.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     lib.muspace_probe_lds_atomic.restype = ctypes.c_int
     lib.muspace_probe_lds_atomic.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                              ctypes.c_int, ctypes.c_void_p]
@@ -722,6 +725,45 @@ def run_lds_atomic_probe() -> dict:
 
 
 PROBE_MIB = (1, 2, 4, 8, 16)  # footprint per XCD
+SCATTER_PROBE_MIB = (0.25, 0.5, 1, 2, 4, 8, 16)  # records * 12 bytes per XCD
+
+
+def run_scatter_probe() -> dict:
+    """Scattered 12-byte records (a 4-byte and an 8-byte store to random
+    records of two arrays, like the tile backward's direct location and weight
+    gradient writes), every workgroup in its own XCD's region of 0.25-16 MiB;
+    2048 workgroups of 256 threads, 32 records a lane. Reports records per
+    second and the time c2's 15.36 M samples' records take at that rate."""
+    lib = probe_library()
+    blocks, iters = 2048, 32
+    stream = torch.cuda.current_stream().cuda_stream
+    max_records = int(max(SCATTER_PROBE_MIB) * (1 << 20)) // 12
+    ga = torch.zeros(8 * max_records, device="cuda")
+    gl = torch.zeros(8 * max_records, 2, device="cuda")
+    rows = {}
+    for mib in SCATTER_PROBE_MIB:
+        records = int(mib * (1 << 20)) // 12
+
+        def launch():
+            rc = lib.muspace_probe_scatter(ga.data_ptr(), gl.data_ptr(), records, blocks, iters,
+                                           stream)
+            assert rc == 0, rc
+        launch()
+        torch.cuda.synchronize()
+        reps = 5
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            launch()
+        end.record()
+        end.synchronize()
+        ms = start.elapsed_time(end) / reps
+        per_s = blocks * 256 * iters / (ms * 1e-3)
+        row = {"us": round(ms * 1e3, 1), "G_records_per_s": round(per_s / 1e9, 1),
+               "us_for_c2_samples": round(15_360_000 / per_s * 1e6, 1)}
+        rows[f"{mib}MiB_per_xcd"] = row
+        print(f"[probe] scatter {mib} MiB/XCD: {row}", file=sys.stderr, flush=True)
+    return {"scatter_probe": rows}
 
 
 def run_probe(kind: str) -> dict:
@@ -807,6 +849,9 @@ def main() -> int:
                         help="time fp32 against u32 LDS atomic adds and exit")
     parser.add_argument("--atomic-probe", action="store_true",
                         help="only the line-wide fp32 atomic-add probe, then exit")
+    parser.add_argument("--scatter-probe", action="store_true",
+                        help="only the scattered 12-byte record store probe (the tile "
+                             "backward's direct gradient writes), then exit")
     parser.add_argument("--sca-only", action="store_true",
                         help="only the fused spatial cross-attention scatter-average leg")
     parser.add_argument("--dfa-only", action="store_true",
@@ -841,13 +886,15 @@ def main() -> int:
         print(json.dumps({"copy_probe_bytes": n * 4, "launches": 5}))
         return 0
 
-    if args.gather_probe or args.atomic_probe or args.lds_atomic_probe:
+    if args.gather_probe or args.atomic_probe or args.lds_atomic_probe or args.scatter_probe:
         out = {}
         for kind, wanted in (("gather", args.gather_probe), ("atomic", args.atomic_probe)):
             if wanted:
                 out.update(run_probe(kind))
         if args.lds_atomic_probe:
             out.update(run_lds_atomic_probe())
+        if args.scatter_probe:
+            out.update(run_scatter_probe())
         print(json.dumps(out))
         return 0
 

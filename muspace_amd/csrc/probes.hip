@@ -8,7 +8,10 @@
 //               the rate of a reference-style atomic grad_value scatter;
 //   lds atomic  fp32 (ds_add_f32) and u32 (ds_add_u32) atomic adds to LDS,
 //               bank-conflict-free or scattered addresses, the rate an
-//               LDS-accumulated grad_value would run at.
+//               LDS-accumulated grad_value would run at;
+//   scatter     a 4-byte and an 8-byte store per record to random records of
+//               two arrays, the tile backward's direct location and weight
+//               gradient writes.
 //
 // Each workgroup works in the region of the XCD it runs on (hardware
 // register XCC_ID), so `lines` per XCD sets the footprint one L2 sees.
@@ -66,6 +69,22 @@ __global__ void __launch_bounds__(kProbeBlock)
     const uint32_t line = mix(wave * 2u + half + 0x632BE5ABu * static_cast<uint32_t>(it)) % lines;
     __hip_atomic_fetch_add(region + static_cast<size_t>(line) * 32 + c, 1.0f, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Scattered records: every lane stores a 4-byte and an 8-byte value to a
+// random record of its XCD's region (`records` records of each array) per
+// step, so the footprint one L2 sees is records * 12 bytes.
+__global__ void __launch_bounds__(kProbeBlock)
+    probe_scatter12(float *__restrict__ ga, float2 *__restrict__ gl, uint32_t records, int iters) {
+  const size_t x = xcd_id();
+  float *ra = ga + x * records;
+  float2 *rl = gl + x * records;
+  const uint32_t t = blockIdx.x * kProbeBlock + threadIdx.x;
+  for (int it = 0; it < iters; ++it) {
+    const uint32_t r = mix(t + 0x632BE5ABu * static_cast<uint32_t>(it)) % records;
+    ra[r] = 1.0f;
+    rl[r] = make_float2(2.0f, 3.0f);
   }
 }
 
@@ -161,6 +180,20 @@ __attribute__((visibility("default"))) int muspace_probe_lds_atomic(uint32_t *ou
   } else {
     probe_lds_atomic<<<blocks, 1024, 0, static_cast<hipStream_t>(stream)>>>(out, iters, kind);
   }
+  return hipGetLastError();
+}
+
+// ga: 8 * records floats, gl: 8 * records float2; each lane stores iters
+// records. Returns a hipError_t.
+__attribute__((visibility("default"))) int muspace_probe_scatter(float *ga, void *gl,
+                                                                 uint64_t records, int blocks,
+                                                                 int iters, void *stream) {
+  if (ga == nullptr || gl == nullptr || records == 0 || records > (1u << 28) || blocks <= 0 ||
+      iters <= 0) {
+    return hipErrorInvalidValue;
+  }
+  probe_scatter12<<<blocks, kProbeBlock, 0, static_cast<hipStream_t>(stream)>>>(
+      ga, static_cast<float2 *>(gl), static_cast<uint32_t>(records), iters);
   return hipGetLastError();
 }
 
